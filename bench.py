@@ -1,0 +1,194 @@
+"""Benchmark of the fused 28-field embedding-bag step on one MI355X.
+
+A step pools one batch of the bf16-2m workload: 28 fields, bf16 tables of 2,000,000 x 128,
+B = 4096 samples, geometric(mean 8) bag lengths, Zipf(1.1) ids, mean pooling, bf16 output
+[4096, 28*128]. Tables and several independently seeded index sets (each with its own hot rows)
+are resident in HBM before timing; step k uses index set k mod n_sets, so consecutive steps do
+not find each other's rows in L2 / MALL.
+
+Printed (one JSON line): pooled bags/s over the timed steps, plus
+  roofline     algorithmic bytes per launch / mean launch duration (HIP events around every
+               launch on the stream the kernel runs on), against 8 TB/s; `traffic` is the HBM
+               traffic per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed
+               under profiles/ (null when absent)
+  cpu_baseline the reference's CPU pooling loop (F.embedding_bag per field, the oracle's
+               restatement) on this host, on a bounded sample of the same batch
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "pooled bags/sec + achieved HBM GB/s (% of peak), B=4096×28 fields, D=128 bf16"
+WORKLOAD_TEXT = {
+    "bf16-2m": "28 fields, bf16 tables 2,000,000 x 128, B=4096, geometric(mean 8) bag lengths clipped to "
+               "[0, 256], Zipf(1.1) ids, mean pooling, bf16 output [4096, 28, 128]",
+    "fp32-1m": "28 fields, fp32 tables 1,000,000 x 128, B=4096, geometric(mean 8) lengths, Zipf(1.1) ids, sum",
+    "hetero-bf16": "28 fields, bf16 tables of width 32/64/128, log-uniform vocab [1e3, 5e6], B=8192, "
+                   "20 Poisson(2) + 8 lognormal(median 64, max 2048) fields, sum",
+    "lazy-32k": "28 fields, bf16 tables 4,000,000 x 128, B=32768 from 8 merged sub-batches, Zipf(0.8), mean",
+    "small-fp32": "28 fields, fp32 tables 10,000 x 64, B=256, Poisson(3) lengths, sum",
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def traffic_from_profiles(workload):
+    """HBM bytes per launch recorded by the rocprofv3 counter runs (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        rec = json.load(fh)
+    return rec.get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(wl, tables_dev, seconds):
+    """Time the oracle's F.embedding_bag loop on host tables holding the rows this batch reads
+    (full-size tables, untouched rows left as zero pages), for about `seconds` of CPU work."""
+    import numpy as np
+    import torch
+
+    from oracle import cpu_loops
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    host = []
+    for f, t in enumerate(tables_dev):
+        s, e = int(wl.offsets[f * wl.batch]), int(wl.offsets[(f + 1) * wl.batch])
+        rows = np.unique(np.clip(wl.values[s:e], 0, wl.vocab[f] - 1))
+        data = t.index_select(0, torch.from_numpy(rows).to(t.device)).cpu()
+        if t.dtype == torch.float32:
+            h = torch.from_numpy(np.zeros(tuple(t.shape), np.float32))
+        else:
+            h = torch.from_numpy(np.zeros(tuple(t.shape), np.int16)).view(t.dtype)
+        h[torch.from_numpy(rows)] = data
+        host.append(h)
+    values = torch.from_numpy(wl.values)
+    offsets = torch.from_numpy(wl.offsets)
+    cpu_loops.embedding_bag_loop(values, offsets, host, wl.pooling, wl.batch)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        cpu_loops.embedding_bag_loop(values, offsets, host, wl.pooling, wl.batch)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 1000:
+            break
+    return {"value": n * wl.num_bags / el, "unit": "bags/s", "cores": threads, "kind": "port",
+            "sample": f"{n} full passes of the timed batch ({wl.num_bags} bags each) in {el:.1f} s through "
+                      f"F.embedding_bag per field (oracle/cpu_loops.py), {wl.table_dtype} tables in host memory"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="bf16-2m", choices=sorted(WORKLOAD_TEXT))
+    ap.add_argument("--sets", type=int, default=8, help="independently seeded index sets rotated over")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--long-threshold", type=int, default=0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE={world}).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from __graft_entry__ import load_package
+
+    pkg = load_package()
+    W = pkg.workloads
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    log(f"workload {args.workload}: generating {args.sets} index sets")
+    wls = [W.make(args.workload, seed=s) for s in range(1, args.sets + 1)]
+    wl0 = wls[0]
+    log("filling tables on the device")
+    tables = W.make_tables(wl0, dev, seed=0)
+    inputs = [W.to_device(wl, dev) for wl in wls]
+    plan = pkg.PooledEmbedding(tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype, long_threshold=args.long_threshold)
+    out = torch.empty((wl0.batch, sum(wl0.dims)), dtype=wl0.out_dtype, device=dev)
+    bytes_alg = [wl.bytes_algorithmic() for wl in wls]
+    bytes_comp = [wl.bytes_compulsory() for wl in wls]
+    torch.cuda.synchronize()
+
+    log(f"warmup {args.warmup} steps")
+    for i in range(args.warmup):
+        v, o = inputs[i % args.sets]
+        plan(v, o, out)
+    torch.cuda.synchronize()
+
+    K = args.steps
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    log(f"timing {K} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        v, o = inputs[i % args.sets]
+        starts[i].record()
+        plan(v, o, out)
+        ends[i].record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    mean_launch_s = float(np.mean(launch_ms)) / 1e3
+    used_bytes = float(np.mean([bytes_alg[i % args.sets] for i in range(K)]))
+    used_comp = float(np.mean([bytes_comp[i % args.sets] for i in range(K)]))
+    ms_per_step = elapsed / K * 1e3
+    value = wl0.num_bags / (elapsed / K)
+    achieved = used_bytes / mean_launch_s / 1e9
+    log(f"{ms_per_step * 1e3:.1f} us/step, launch {mean_launch_s * 1e6:.1f} us (median "
+        f"{np.median(launch_ms) * 1e3:.1f}), {achieved:.0f} GB/s algorithmic, "
+        f"{used_comp / mean_launch_s / 1e9:.0f} GB/s compulsory")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(wl0, tables, args.cpu_seconds)
+
+    rec = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "bags/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[wl0.table_dtype],
+        "data": f"synthetic: {args.sets} seeded index sets rotated, random N(0, 0.01) tables",
+        "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}", "batch": wl0.batch,
+                   "fields": wl0.num_fields, "dims": sorted(set(wl0.dims)), "pooling": wl0.pooling,
+                   "nnz_mean": float(np.mean([wl.nnz for wl in wls])), "index_sets": args.sets},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profiles(args.workload),
+                     "kernel": "pool_kernel", "bytes_per_launch": used_bytes,
+                     "compulsory_bytes_per_launch": used_comp, "launch_us_mean": mean_launch_s * 1e6,
+                     "launch_us_median": float(np.median(launch_ms)) * 1e3},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,31 @@
+"""MI355X-native fused sparse-feature embedding-bag path (hand-written HIP kernels for gfx950).
+
+Public surface:
+  fused_all_slots_embedding  drop-in for the reference's fused_all_slots_embedding_kernel launch
+  fused_embedding            the RepEncoder.forward fused step on a flat-layout batch dict
+  embedding_bag_pooled       per-field tables, global offsets, sum/mean, chosen output dtype
+  PooledEmbedding            the same with the table descriptors prepared once (serving loops)
+  RepEncoder                 the reference module with the fused step on this path
+  collate_flat_layout, prebuild_flat_layout   host builders of the flat layout
+  pack_slots, merge_batches                   GPU builders of the flat layout
+"""
+from . import workloads
+from ._capi import EbagError, lib as load_library
+from .encoder import RepEncoder
+from .layout import collate_flat_layout, merge_batches, pack_slots, prebuild_flat_layout
+from .ops import PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_embedding
+
+__all__ = [
+    "EbagError",
+    "load_library",
+    "RepEncoder",
+    "collate_flat_layout",
+    "prebuild_flat_layout",
+    "pack_slots",
+    "merge_batches",
+    "embedding_bag_pooled",
+    "PooledEmbedding",
+    "fused_all_slots_embedding",
+    "fused_embedding",
+    "workloads",
+]

@@ -1,0 +1,192 @@
+// Device helpers shared by the embedding-bag kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace cti {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------------------------
+// Element types. Tables and outputs are raw 16-bit / 32-bit words; conversions are explicit.
+// ---------------------------------------------------------------------------------------------
+struct bf16_t {
+  uint16_t bits;
+};
+struct f16_t {
+  uint16_t bits;
+};
+
+// bf16 -> fp32 is exact: the bf16 word is the high half of the fp32 word.
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16, IEEE round-to-nearest-even on the 16 discarded bits. NaN stays NaN (quiet bit
+// forced) with its sign; +-Inf and values that round past the largest finite bf16 become +-Inf.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x0040u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return __half2float(__ushort_as_half(static_cast<unsigned short>(h)));
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  static constexpr int kBytes = 4;
+  __device__ static __forceinline__ float load(const void* p) { return *static_cast<const float*>(p); }
+};
+template <>
+struct Elem<bf16_t> {
+  static constexpr int kBytes = 2;
+  __device__ static __forceinline__ float load(const void* p) {
+    return bf16_bits_to_f32(*static_cast<const uint16_t*>(p));
+  }
+};
+template <>
+struct Elem<f16_t> {
+  static constexpr int kBytes = 2;
+  __device__ static __forceinline__ float load(const void* p) {
+    return f16_bits_to_f32(*static_cast<const uint16_t*>(p));
+  }
+};
+
+// Add the elements held in one 16-byte vector to fp32 accumulators, in element order.
+__device__ __forceinline__ void acc16(float* a, const uint4& v, float) {
+  a[0] += __uint_as_float(v.x);
+  a[1] += __uint_as_float(v.y);
+  a[2] += __uint_as_float(v.z);
+  a[3] += __uint_as_float(v.w);
+}
+__device__ __forceinline__ void acc16(float* a, const uint4& v, bf16_t) {
+  a[0] += __uint_as_float(v.x << 16);
+  a[1] += __uint_as_float(v.x & 0xffff0000u);
+  a[2] += __uint_as_float(v.y << 16);
+  a[3] += __uint_as_float(v.y & 0xffff0000u);
+  a[4] += __uint_as_float(v.z << 16);
+  a[5] += __uint_as_float(v.z & 0xffff0000u);
+  a[6] += __uint_as_float(v.w << 16);
+  a[7] += __uint_as_float(v.w & 0xffff0000u);
+}
+__device__ __forceinline__ void acc16(float* a, const uint4& v, f16_t) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[2 * i] += f16_bits_to_f32(w[i] & 0xffffu);
+    a[2 * i + 1] += f16_bits_to_f32(w[i] >> 16);
+  }
+}
+
+// Store N fp32 values as output type OT (N * sizeof(OT) is a multiple of 8 bytes and the
+// destination is aligned to that size by the host-side variant selection).
+template <int N>
+__device__ __forceinline__ void store_out(float* dst, const float* a) {
+  static_assert(N % 4 == 0, "fp32 stores are 16-byte vectors");
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    uint4 v;
+    v.x = __float_as_uint(a[i]);
+    v.y = __float_as_uint(a[i + 1]);
+    v.z = __float_as_uint(a[i + 2]);
+    v.w = __float_as_uint(a[i + 3]);
+    *reinterpret_cast<uint4*>(dst + i) = v;
+  }
+}
+template <int N>
+__device__ __forceinline__ void store_out(bf16_t* dst, const float* a) {
+  static_assert(N % 4 == 0, "16-bit stores are 8- or 16-byte vectors");
+  if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 8) {
+      uint4 v;
+      v.x = f32_to_bf16_bits(a[i]) | (f32_to_bf16_bits(a[i + 1]) << 16);
+      v.y = f32_to_bf16_bits(a[i + 2]) | (f32_to_bf16_bits(a[i + 3]) << 16);
+      v.z = f32_to_bf16_bits(a[i + 4]) | (f32_to_bf16_bits(a[i + 5]) << 16);
+      v.w = f32_to_bf16_bits(a[i + 6]) | (f32_to_bf16_bits(a[i + 7]) << 16);
+      *reinterpret_cast<uint4*>(dst + i) = v;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      uint2 v;
+      v.x = f32_to_bf16_bits(a[i]) | (f32_to_bf16_bits(a[i + 1]) << 16);
+      v.y = f32_to_bf16_bits(a[i + 2]) | (f32_to_bf16_bits(a[i + 3]) << 16);
+      *reinterpret_cast<uint2*>(dst + i) = v;
+    }
+  }
+}
+template <int N>
+__device__ __forceinline__ void store_out(f16_t* dst, const float* a) {
+  static_assert(N % 4 == 0, "16-bit stores are 8- or 16-byte vectors");
+  if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 8) {
+      uint4 v;
+      v.x = f32_to_f16_bits(a[i]) | (f32_to_f16_bits(a[i + 1]) << 16);
+      v.y = f32_to_f16_bits(a[i + 2]) | (f32_to_f16_bits(a[i + 3]) << 16);
+      v.z = f32_to_f16_bits(a[i + 4]) | (f32_to_f16_bits(a[i + 5]) << 16);
+      v.w = f32_to_f16_bits(a[i + 6]) | (f32_to_f16_bits(a[i + 7]) << 16);
+      *reinterpret_cast<uint4*>(dst + i) = v;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      uint2 v;
+      v.x = f32_to_f16_bits(a[i]) | (f32_to_f16_bits(a[i + 1]) << 16);
+      v.y = f32_to_f16_bits(a[i + 2]) | (f32_to_f16_bits(a[i + 3]) << 16);
+      *reinterpret_cast<uint2*>(dst + i) = v;
+    }
+  }
+}
+
+__device__ __forceinline__ void store_one(float* dst, float a) { *dst = a; }
+__device__ __forceinline__ void store_one(bf16_t* dst, float a) {
+  *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(f32_to_bf16_bits(a));
+}
+__device__ __forceinline__ void store_one(f16_t* dst, float a) {
+  *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(f32_to_f16_bits(a));
+}
+
+// ---------------------------------------------------------------------------------------------
+// Cross-lane moves inside one wavefront (ds_bpermute: any-to-any, all 64 lanes must be active).
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+__device__ __forceinline__ int shfl_i32(int v, int src_lane) {
+  return __builtin_amdgcn_ds_bpermute(src_lane << 2, v);
+}
+__device__ __forceinline__ int64_t shfl_i64(int64_t v, int src_lane) {
+  const int lo = shfl_i32(static_cast<int>(static_cast<uint64_t>(v)), src_lane);
+  const int hi = shfl_i32(static_cast<int>(static_cast<uint64_t>(v) >> 32), src_lane);
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                              static_cast<uint32_t>(lo));
+}
+__device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
+  return __int_as_float(shfl_i32(__float_as_int(v), lane_id() ^ mask));
+}
+__device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const int64_t o = shfl_i64(v, lane_id() ^ m);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint4 load16(const char* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+__device__ __forceinline__ int64_t clamp_i64(int64_t v, int64_t lo, int64_t hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+}  // namespace cti

@@ -1,0 +1,61 @@
+"""RepEncoder with the fused embedding step on the HIP path.
+
+Mirrors the reference module online_best/infer.py:945-1100 (constructor signature, parameter
+names, forward(batch) contract): the 28 slots are pooled by ``fused_all_slots_embedding`` into
+``[B, slot_num*emb_dim]`` in the table's dtype, then LayerNorm(slot_num*emb_dim) and
+Linear(slot_num*emb_dim -> d_model) follow, as at online_best/infer.py:1061-1085.
+
+The LayerNorm and Linear here are torch's modules: they are downstream of the pooled output,
+whose layout (contiguous rows of slot_num*emb_dim, slot-major columns) is what this module
+guarantees them (online_best/infer.py:836-843).
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .layout import pack_slots
+from .ops import fused_all_slots_embedding
+
+
+class RepEncoder(nn.Module):
+    def __init__(self, vocab_size, emb_dim, padding_idx=0, slot_num=0, d_model=0):
+        super().__init__()
+        self.emb = nn.Embedding(num_embeddings=vocab_size, embedding_dim=emb_dim, padding_idx=padding_idx)
+        self.emb_dim = emb_dim
+        self.slot_num = slot_num
+        self.input_norm = nn.LayerNorm(slot_num * emb_dim)
+        self.linear = nn.Linear(in_features=slot_num * emb_dim, out_features=d_model)
+
+    def flat_inputs(self, batch: dict):
+        """(flat_values, val_offsets, flat_row_offsets, batch_size) of a batch.
+
+        Batches that carry only the int-keyed per-slot pairs are packed on the GPU
+        (online_best/infer.py:960-974); B comes from the offsets length (online_best/infer.py:1033).
+        """
+        if "_flat_values" not in batch:
+            device = self.emb.weight.device
+            slots = []
+            for i in range(self.slot_num):
+                vals, offs = batch[i + 1]
+                slots.append((vals.to(device), offs.to(device)))
+            batch = pack_slots(slots)
+        flat_values = batch["_flat_values"]
+        flat_row_offsets = batch["_flat_row_offsets"]
+        val_offsets = batch["_val_offsets"]
+        batch_size = flat_row_offsets.shape[0] // self.slot_num - 1
+        return flat_values, val_offsets, flat_row_offsets, batch_size
+
+    def pooled(self, batch: dict) -> torch.Tensor:
+        """The fused embedding step: ``[B, slot_num*emb_dim]`` in the table dtype."""
+        flat_values, val_offsets, flat_row_offsets, batch_size = self.flat_inputs(batch)
+        weight = self.emb.weight
+        out = torch.empty((batch_size, self.slot_num * self.emb_dim), device=weight.device, dtype=weight.dtype)
+        with torch.no_grad():
+            return fused_all_slots_embedding(flat_values, val_offsets, flat_row_offsets, weight.detach(), out,
+                                             batch_size, self.emb_dim, self.emb.num_embeddings - 1)
+
+    def forward(self, batch: dict) -> torch.Tensor:
+        fused_embs = self.pooled(batch)
+        norm_emb = self.input_norm(fused_embs)
+        return self.linear(norm_emb)

@@ -1,0 +1,257 @@
+"""Host entry points of the fused sparse-feature embedding-bag path.
+
+``fused_all_slots_embedding`` is the drop-in for the reference launch
+``fused_all_slots_embedding_kernel[(B, 28)](values, val_offsets, row_offsets, weight, out,
+batch_size, emb_dim, max_idx, BLOCK_SIZE)`` (online_best/infer.py:793-827, launched at
+online_best/infer.py:1052-1059): same arguments in the same order (grid and BLOCK_SIZE are
+chosen inside), same layout, same results, launched on torch's current stream.
+
+``embedding_bag_pooled`` is the general form: per-field tables (possibly of different widths),
+global offsets ``offsets[F*B+1]``, sum or mean pooling, and an explicit output dtype.
+
+Both validate their arguments on the host (no device synchronisation) and raise ``ValueError``
+/ ``TypeError`` for malformed calls and ``EbagError`` when the C ABI reports a failure.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import torch
+
+from . import _capi
+
+
+def _require_device_tensor(name: str, t: torch.Tensor, device: Optional[torch.device] = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (got device {t.device})")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def _require_contiguous(name: str, t: torch.Tensor) -> None:
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def fused_all_slots_embedding(
+    flat_values: torch.Tensor,
+    val_offsets: torch.Tensor,
+    flat_row_offsets: torch.Tensor,
+    weight: torch.Tensor,
+    out: torch.Tensor,
+    batch_size: int,
+    emb_dim: int,
+    max_idx: int,
+) -> torch.Tensor:
+    """Pool every slot of a flat-layout batch into ``out[B, S*emb_dim]`` (sum, fp32 accumulate).
+
+    Arguments mirror online_best/infer.py:794-804:
+      flat_values       int64 [nnz]        field-major sign ids (online_best/infer.py:471)
+      val_offsets       int64 [S]          slot starts in flat_values (online_best/infer.py:473)
+      flat_row_offsets  int64 [S*(B+1)]    per-slot local offsets (online_best/infer.py:472)
+      weight            [V, emb_dim]       shared table (fp32 / bf16 / fp16), contiguous
+      out               [B, S*emb_dim]     caller-allocated, weight's dtype (online_best/infer.py:1050)
+      batch_size        B
+      emb_dim           D
+      max_idx           clamp bound, V-1 in the reference (online_best/infer.py:1057)
+    Returns ``out``.
+    """
+    dev = weight.device
+    _require_device_tensor("weight", weight)
+    for name, t in (("flat_values", flat_values), ("val_offsets", val_offsets),
+                    ("flat_row_offsets", flat_row_offsets), ("out", out)):
+        _require_device_tensor(name, t, dev)
+        _require_contiguous(name, t)
+    for name, t in (("flat_values", flat_values), ("val_offsets", val_offsets),
+                    ("flat_row_offsets", flat_row_offsets)):
+        if t.dtype != torch.int64:
+            raise TypeError(f"{name} must be int64 (got {t.dtype})")
+    if weight.dim() != 2:
+        raise ValueError(f"weight must be 2-D [V, D], got shape {tuple(weight.shape)}")
+    _require_contiguous("weight", weight)
+    batch_size = int(batch_size)
+    emb_dim = int(emb_dim)
+    max_idx = int(max_idx)
+    num_slots = val_offsets.numel()
+    if weight.shape[1] != emb_dim:
+        raise ValueError(f"weight has {weight.shape[1]} columns, emb_dim is {emb_dim}")
+    if not 0 <= max_idx < weight.shape[0]:
+        raise ValueError(f"max_idx {max_idx} outside [0, {weight.shape[0] - 1}]")
+    if batch_size < 0:
+        raise ValueError(f"batch_size must be >= 0, got {batch_size}")
+    if flat_row_offsets.numel() != num_slots * (batch_size + 1):
+        raise ValueError(
+            f"flat_row_offsets has {flat_row_offsets.numel()} entries, expected "
+            f"{num_slots} * ({batch_size} + 1)"
+        )
+    if out.dtype != weight.dtype:
+        raise TypeError(f"out dtype {out.dtype} differs from weight dtype {weight.dtype}")
+    if out.numel() != batch_size * num_slots * emb_dim or (out.dim() >= 1 and out.shape[0] != batch_size):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected ({batch_size}, {num_slots * emb_dim})")
+    lib = _capi.lib()
+    with torch.cuda.device(dev):
+        stream = _capi.current_stream_handle(dev)
+        _capi.check(lib.cti_ebag_fused_all_slots(
+            flat_values.data_ptr(), val_offsets.data_ptr(), flat_row_offsets.data_ptr(),
+            weight.data_ptr(), _capi.dtype_code(weight.dtype), out.data_ptr(),
+            batch_size, num_slots, emb_dim, max_idx, flat_values.numel(), stream))
+    return out
+
+
+def fused_embedding(batch: dict, weight: torch.Tensor, slot_num: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The fused embedding step of RepEncoder.forward (online_best/infer.py:1029-1059) on a
+    batch dict holding ``_flat_values``, ``_flat_row_offsets`` and ``_val_offsets``.
+
+    B is derived from the offsets length as at online_best/infer.py:1033; ``out`` is allocated
+    in the weight dtype when not given (online_best/infer.py:1050-1051).
+    """
+    flat_values = batch["_flat_values"]
+    flat_row_offsets = batch["_flat_row_offsets"]
+    val_offsets = batch["_val_offsets"]
+    batch_size = flat_row_offsets.shape[0] // slot_num - 1
+    emb_dim = weight.shape[1]
+    if out is None:
+        out = torch.empty((batch_size, slot_num * emb_dim), device=weight.device, dtype=weight.dtype)
+    return fused_all_slots_embedding(flat_values, val_offsets, flat_row_offsets, weight, out,
+                                     batch_size, emb_dim, weight.shape[0] - 1)
+
+
+def embedding_bag_pooled(
+    values: torch.Tensor,
+    offsets: torch.Tensor,
+    tables: Sequence[torch.Tensor],
+    pooling: str = "sum",
+    out_dtype: Optional[torch.dtype] = None,
+    out: Optional[torch.Tensor] = None,
+    long_threshold: int = 0,
+) -> torch.Tensor:
+    """Pool F fields with per-field tables into ``out[B, sum(D_f)]``.
+
+      values   int64 or int32 [nnz], field-major
+      offsets  int64 [F*B+1]; bag (f, b) = values[offsets[f*B+b] : offsets[f*B+b+1]]
+      tables   F row-major 2-D tensors [V_f, D_f] of one dtype (fp32 / bf16 / fp16); row
+               stride may exceed D_f. Field f fills columns [sum_{g<f} D_g, ... + D_f).
+      pooling  'sum' or 'mean' (mean of an empty bag is 0)
+      out_dtype defaults to the tables' dtype; ``out`` (if given) must be contiguous
+               [B, sum(D_f)] of that dtype.
+      long_threshold  bags longer than this are split across a workgroup's 4 wavefronts
+               (0 = per-shape default, -1 = split every non-empty bag).
+    Equivalent to, per field, F.embedding_bag(clamp(values_f, 0, V_f-1), table_f, offsets_f,
+    mode=pooling) followed by concatenation along dim 1 (baseline/infer.py:256-263).
+    """
+    num_fields = len(tables)
+    if num_fields == 0:
+        raise ValueError("at least one table is required")
+    dev = tables[0].device
+    tdt = tables[0].dtype
+    for i, t in enumerate(tables):
+        _require_device_tensor(f"tables[{i}]", t, dev)
+        if t.dim() != 2:
+            raise ValueError(f"tables[{i}] must be 2-D, got shape {tuple(t.shape)}")
+        if t.dtype != tdt:
+            raise TypeError(f"tables[{i}] dtype {t.dtype} differs from tables[0] dtype {tdt}")
+        if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+            raise ValueError(f"tables[{i}] must be row-major with unit column stride")
+        if t.shape[0] < 1:
+            raise ValueError(f"tables[{i}] has no rows")
+    _require_device_tensor("values", values, dev)
+    _require_device_tensor("offsets", offsets, dev)
+    _require_contiguous("values", values)
+    _require_contiguous("offsets", offsets)
+    if offsets.dtype != torch.int64:
+        raise TypeError(f"offsets must be int64 (got {offsets.dtype})")
+    if (offsets.numel() - 1) % num_fields != 0 or offsets.numel() < 1:
+        raise ValueError(f"offsets has {offsets.numel()} entries; expected F*B+1 with F={num_fields}")
+    batch_size = (offsets.numel() - 1) // num_fields
+    dims = [int(t.shape[1]) for t in tables]
+    width = sum(dims)
+    odt = tdt if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((batch_size, width), device=dev, dtype=odt)
+    else:
+        _require_device_tensor("out", out, dev)
+        _require_contiguous("out", out)
+        if out.dtype != odt:
+            raise TypeError(f"out dtype {out.dtype} differs from requested {odt}")
+        if tuple(out.shape) != (batch_size, width):
+            raise ValueError(f"out has shape {tuple(out.shape)}, expected ({batch_size}, {width})")
+    descs = (_capi.Table * num_fields)()
+    col = 0
+    for i, t in enumerate(tables):
+        descs[i].data = t.data_ptr()
+        descs[i].rows = t.shape[0]
+        descs[i].row_stride = t.stride(0)
+        descs[i].dim = dims[i]
+        descs[i].out_col = col
+        col += dims[i]
+    opts = _capi.Options()
+    opts.long_threshold = int(long_threshold)
+    opts.use_bins = 0
+    lib = _capi.lib()
+    with torch.cuda.device(dev):
+        stream = _capi.current_stream_handle(dev)
+        _capi.check(lib.cti_ebag_forward(
+            values.data_ptr(), _capi.index_code(values.dtype), values.numel(), offsets.data_ptr(),
+            batch_size, num_fields, descs, _capi.dtype_code(tdt), _capi.pooling_code(pooling),
+            out.data_ptr(), _capi.dtype_code(odt), width, None, 0, ctypes.byref(opts), stream))
+    return out
+
+
+class PooledEmbedding:
+    """A prepared call of the general entry point for fixed tables: the table descriptors and
+    options are built once, so each call costs one C-ABI call (a few microseconds on the host).
+
+    ``plan(values, offsets, out=None)`` pools one batch exactly as embedding_bag_pooled would.
+    """
+
+    def __init__(self, tables: Sequence[torch.Tensor], pooling: str = "sum",
+                 out_dtype: Optional[torch.dtype] = None, long_threshold: int = 0):
+        if len(tables) == 0:
+            raise ValueError("at least one table is required")
+        self.tables = list(tables)
+        self.device = self.tables[0].device
+        tdt = self.tables[0].dtype
+        for i, t in enumerate(self.tables):
+            _require_device_tensor(f"tables[{i}]", t, self.device)
+            if t.dim() != 2 or t.dtype != tdt or t.stride(1) != 1 or t.stride(0) < t.shape[1] or t.shape[0] < 1:
+                raise ValueError(f"tables[{i}] must be a non-empty row-major 2-D tensor of dtype {tdt}")
+        self.num_fields = len(self.tables)
+        self.width = sum(int(t.shape[1]) for t in self.tables)
+        self.table_dtype = tdt
+        self.out_dtype = tdt if out_dtype is None else out_dtype
+        self._tdt = _capi.dtype_code(tdt)
+        self._odt = _capi.dtype_code(self.out_dtype)
+        self._pool = _capi.pooling_code(pooling)
+        self._descs = (_capi.Table * self.num_fields)()
+        col = 0
+        for i, t in enumerate(self.tables):
+            d = self._descs[i]
+            d.data, d.rows, d.row_stride, d.dim, d.out_col = t.data_ptr(), t.shape[0], t.stride(0), t.shape[1], col
+            col += int(t.shape[1])
+        self._opts = _capi.Options()
+        self._opts.long_threshold = int(long_threshold)
+        self._lib = _capi.lib()
+        self._fn = self._lib.cti_ebag_forward
+
+    def __call__(self, values: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if values.device != self.device or offsets.device != self.device:
+            raise ValueError(f"values and offsets must be on {self.device}")
+        if offsets.dtype != torch.int64 or not offsets.is_contiguous() or not values.is_contiguous():
+            raise ValueError("offsets must be contiguous int64 and values contiguous")
+        n_off = offsets.numel()
+        if n_off < 1 or (n_off - 1) % self.num_fields:
+            raise ValueError(f"offsets has {n_off} entries; expected F*B+1 with F={self.num_fields}")
+        batch = (n_off - 1) // self.num_fields
+        if out is None:
+            out = torch.empty((batch, self.width), device=self.device, dtype=self.out_dtype)
+        elif out.dtype != self.out_dtype or tuple(out.shape) != (batch, self.width) or not out.is_contiguous() \
+                or out.device != self.device:
+            raise ValueError(f"out must be a contiguous ({batch}, {self.width}) {self.out_dtype} tensor on {self.device}")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        _capi.check(self._fn(values.data_ptr(), _capi.index_code(values.dtype), values.numel(), offsets.data_ptr(),
+                             batch, self.num_fields, self._descs, self._tdt, self._pool, out.data_ptr(), self._odt,
+                             self.width, None, 0, self._opts, stream))
+        return out

@@ -1,0 +1,176 @@
+/*
+ * cti_ebag.h — C ABI of the MI355X (gfx950) fused sparse-feature embedding-bag path.
+ *
+ * The path pools F variable-length sparse fields ("slots") of a batch of B samples into
+ * one dense row per sample:  out[b, col_f : col_f + D_f] = pool_{i in bag(b, f)} table_f[clamp(v_i)].
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   - online_best/infer.py:793-827   Triton kernel fused_all_slots_embedding_kernel
+ *                                    (values_ptr, val_offsets_ptr, row_offsets_ptr, weight_ptr,
+ *                                     out_ptr, batch_size, emb_dim, max_idx, BLOCK_SIZE)
+ *   - online_best/infer.py:1029-1059 its launch from RepEncoder.forward (grid (B, 28),
+ *                                    out allocated by the caller in the weight dtype)
+ *   - online_best/infer.py:960-974   per-slot (values, offsets) -> flat layout (torch.cat on device)
+ *   - online_best/infer.py:581-631   per-field concatenation of K cached sub-batches
+ *   - baseline/infer.py:253-266      per-field clamp + nn.Embedding + segment_reduce(sum) + cat
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless stated otherwise ("host" below).
+ *   - Nothing here allocates device memory, synchronises the host, or throws. Work is
+ *     enqueued on `stream` (a hipStream_t; NULL = the default stream) and runs asynchronously.
+ *   - Return value: CTI_EBAG_OK (0) or a negative CTI_EBAG_E* code; the message of the last
+ *     failure on the calling host thread is returned by cti_ebag_last_error().
+ *   - Argument validation happens on the host before any HIP call, so argument errors are
+ *     reported without touching a GPU.
+ *   - Sign ids are clamped to [0, rows-1] (online_best/infer.py:823, baseline/infer.py:259);
+ *     row 0 is read like any other row (no padding mask in the forward pass).
+ *   - Bag (f, b) with end <= start is empty and pools to exactly 0 (sum and mean).
+ *   - Accumulation is fp32; the result is rounded once to the output dtype
+ *     (round-to-nearest-even for bf16/fp16).
+ *   - Offsets are int64. Offsets outside [0, nnz] are clipped into that range on the device
+ *     (the reference assumes well-formed offsets; clipping keeps a malformed batch from
+ *     reading outside `values`).
+ *   - Calls that share an output buffer or a workspace must not overlap in time.
+ */
+#ifndef CTI_EBAG_H
+#define CTI_EBAG_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CTI_EBAG_ABI_VERSION 1
+
+/* element types of tables and outputs */
+#define CTI_EBAG_F32 0
+#define CTI_EBAG_BF16 1
+#define CTI_EBAG_F16 2
+
+/* index (sign id) types */
+#define CTI_EBAG_I64 0
+#define CTI_EBAG_I32 1
+
+/* pooling modes */
+#define CTI_EBAG_SUM 0
+#define CTI_EBAG_MEAN 1
+
+/* status codes */
+#define CTI_EBAG_OK 0
+#define CTI_EBAG_EINVAL (-1)      /* bad argument (null pointer, negative size, bad enum, ...) */
+#define CTI_EBAG_EUNSUPPORTED (-2) /* well-formed but outside what this build implements */
+#define CTI_EBAG_EHIP (-3)        /* a HIP runtime call failed (message carries hipGetErrorString) */
+#define CTI_EBAG_EWORKSPACE (-4)  /* workspace missing or smaller than cti_ebag_workspace_bytes() */
+
+/* One field's table. `data` is a device pointer to a row-major [rows, row_stride] matrix of
+ * which the first `dim` columns are used. `out_col` is the first output column of the field.
+ * Several fields may share one `data` pointer (the reference's single shared nn.Embedding). */
+typedef struct cti_ebag_table {
+  const void* data;
+  int64_t rows;
+  int64_t row_stride; /* elements between consecutive rows, >= dim */
+  int32_t dim;
+  int32_t out_col;
+} cti_ebag_table;
+
+/* Tuning knobs of one launch. Zero-initialise and set only what you need:
+ *   long_threshold: bags longer than this are split across the 4 wavefronts of a workgroup
+ *                   (partial sums combined through LDS in a fixed order). 0 = default.
+ *                   A negative value splits every non-empty bag (used by tests).
+ *   use_bins:       1 = run the device length-binning pass and visit heavy tiles first;
+ *                   needs a workspace of cti_ebag_workspace_bytes() bytes. 0 = natural order.  */
+typedef struct cti_ebag_options {
+  int32_t long_threshold;
+  int32_t use_bins;
+  int32_t reserved[6];
+} cti_ebag_options;
+
+/* ABI version this library was built with (CTI_EBAG_ABI_VERSION). */
+int cti_ebag_abi_version(void);
+
+/* Message describing the last failure on this host thread ("" if none). */
+const char* cti_ebag_last_error(void);
+
+/*
+ * Reference-layout entry point: a drop-in for the launch
+ *   fused_all_slots_embedding_kernel[(batch_size, num_slots)](values, val_offsets, row_offsets,
+ *       weight, out, batch_size, emb_dim, max_idx, BLOCK_SIZE=next_pow2(emb_dim))
+ * at online_best/infer.py:1052-1059 (kernel body online_best/infer.py:805-827).
+ *
+ *   values      int64 [nnz]                field-major sign ids (online_best/infer.py:471)
+ *   val_offsets int64 [num_slots]          start of each slot inside `values` (:473)
+ *   row_offsets int64 [num_slots*(B+1)]    per-slot local bag offsets, each slot starts at 0 (:472)
+ *   weight      [max_idx+1, emb_dim]       one table shared by all slots, dtype `dtype`
+ *   out         [B, num_slots*emb_dim]     written in `dtype`, slot-major columns (:826)
+ *   nnz         length of `values` (bounds the clipping of malformed offsets)
+ * Sum pooling, fp32 accumulation, result rounded once to `dtype` (:819-827).
+ */
+int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* val_offsets,
+                             const int64_t* row_offsets, const void* weight, int32_t dtype,
+                             void* out, int64_t batch_size, int32_t num_slots, int32_t emb_dim,
+                             int64_t max_idx, int64_t nnz, void* stream);
+
+/*
+ * General entry point (per-field tables, global offsets, sum/mean).
+ *   values        [nnz] sign ids of type `index_type`, field-major
+ *   offsets       int64 [num_fields*B + 1]; bag (f, b) = values[offsets[f*B+b] : offsets[f*B+b+1]]
+ *   tables        host array of num_fields descriptors (read during the call only)
+ *   table_dtype   element type shared by all tables
+ *   pooling       CTI_EBAG_SUM or CTI_EBAG_MEAN (mean of an empty bag is 0)
+ *   out           [B, out_row_stride] of `out_dtype`; field f writes columns
+ *                 [out_col_f, out_col_f + dim_f)
+ *   workspace     device scratch of at least cti_ebag_workspace_bytes(...) bytes when
+ *                 opts->use_bins is set (else may be NULL); contents need no initialisation
+ *   opts          host pointer, may be NULL (all defaults)
+ * Replaces the per-field loop at baseline/infer.py:256-263 and generalises the reference
+ * kernel (online_best/infer.py:805-827) to per-field tables and mean pooling.
+ */
+int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
+                     int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables,
+                     int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
+                     int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                     const cti_ebag_options* opts, void* stream);
+
+/* Bytes of device workspace cti_ebag_forward needs with opts->use_bins = 1. */
+int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fields);
+
+/*
+ * Device packer for the reference flat layout (online_best/infer.py:960-974, and the
+ * host builders :446-474 and :139-154 which produce the same three tensors):
+ *   slot_values[s]  host array of num_slots device pointers, slot s has slot_nnz[s] int64 ids
+ *   slot_offsets[s] host array of num_slots device pointers, each int64 [B+1], starting at 0
+ *   slot_nnz        host array of num_slots counts
+ * Writes flat_values int64 [sum nnz], flat_row_offsets int64 [num_slots*(B+1)],
+ * val_offsets int64 [num_slots] (exclusive prefix of slot_nnz) and, if `global_offsets`
+ * is not NULL, the global form int64 [num_slots*B+1]:
+ *   global_offsets[s*B+b] = val_offsets[s] + row_offsets_s[b],  global_offsets[S*B] = total nnz.
+ */
+int cti_ebag_pack_slots(const int64_t* const* slot_values, const int64_t* const* slot_offsets,
+                        const int64_t* slot_nnz, int32_t num_slots, int64_t batch_size,
+                        int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
+                        int64_t* global_offsets, void* stream);
+
+/*
+ * Device merge of K flat-layout sub-batches into one, field by field in sub-batch order
+ * (online_best/infer.py:581-631, online_best/infer.py:2977-3037):
+ *   sub_values[k], sub_val_offsets[k], sub_row_offsets[k]   host arrays of K device pointers
+ *   sub_batch[k]    host array: samples in sub-batch k;  sub_nnz[k]: length of sub_values[k]
+ * Output: the flat layout of the merged batch with B = sum sub_batch[k]:
+ *   flat_values int64 [sum sub_nnz], flat_row_offsets int64 [num_slots*(B+1)],
+ *   val_offsets int64 [num_slots]; optional global_offsets int64 [num_slots*B+1].
+ * Slot s of sub-batch k spans sub_values[k][val_offsets_k[s] : val_offsets_k[s+1]]
+ * (the last slot ends at sub_nnz[k]), as at online_best/infer.py:604-606.
+ */
+int cti_ebag_merge_batches(const int64_t* const* sub_values,
+                           const int64_t* const* sub_val_offsets,
+                           const int64_t* const* sub_row_offsets, const int64_t* sub_batch,
+                           const int64_t* sub_nnz, int32_t num_sub, int32_t num_slots,
+                           int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
+                           int64_t* global_offsets, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CTI_EBAG_H */

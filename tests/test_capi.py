@@ -1,0 +1,159 @@
+"""The C ABI without a GPU: the library loads, exports what include/cti_ebag.h declares, and
+rejects malformed arguments on the host (no HIP call is reached)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cti_ebag.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cti_ebag_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for n in ("cti_ebag_fused_all_slots", "cti_ebag_forward", "cti_ebag_pack_slots", "cti_ebag_merge_batches",
+              "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg.load_library()
+    raw = ctypes.CDLL(pkg._capi.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+        assert name in pkg._capi.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.cti_ebag_abi_version() == pkg._capi.ABI_VERSION
+    ver = int(re.search(r"#define CTI_EBAG_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert ver == pkg._capi.ABI_VERSION
+
+
+def test_status_codes_match_header(pkg):
+    text = open(HEADER).read()
+    for name in ("OK", "EINVAL", "EUNSUPPORTED", "EHIP", "EWORKSPACE"):
+        v = int(re.search(rf"#define CTI_EBAG_{name} \(?(-?\d+)\)?", text).group(1))
+        assert getattr(pkg._capi, name) == v
+    for name, attr in (("F32", "F32"), ("BF16", "BF16"), ("F16", "F16"), ("I64", "I64"), ("I32", "I32"),
+                       ("SUM", "SUM"), ("MEAN", "MEAN")):
+        v = int(re.search(rf"#define CTI_EBAG_{name} (\d+)", text).group(1))
+        assert getattr(pkg._capi, attr) == v
+
+
+def _forward(pkg, **kw):
+    c = pkg._capi
+    args = dict(values=1, index_type=c.I64, nnz=10, offsets=1, batch=4, num_fields=1, tables=None, tdt=c.BF16,
+                pooling=c.SUM, out=1, odt=c.BF16, stride=128, ws=None, ws_bytes=0, opts=None, stream=None)
+    args.update(kw)
+    return c.lib().cti_ebag_forward(args["values"], args["index_type"], args["nnz"], args["offsets"], args["batch"],
+                                    args["num_fields"], args["tables"], args["tdt"], args["pooling"], args["out"],
+                                    args["odt"], args["stride"], args["ws"], args["ws_bytes"], args["opts"],
+                                    args["stream"])
+
+
+def _table(pkg, **kw):
+    t = (pkg._capi.Table * 1)()
+    t[0].data = kw.get("data", 64)
+    t[0].rows = kw.get("rows", 100)
+    t[0].row_stride = kw.get("row_stride", 128)
+    t[0].dim = kw.get("dim", 128)
+    t[0].out_col = kw.get("out_col", 0)
+    return t
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(index_type=7), "index type"),
+    (dict(tdt=9), "table dtype"),
+    (dict(odt=-1), "output dtype"),
+    (dict(pooling=5), "pooling"),
+    (dict(nnz=-1), "nnz"),
+    (dict(batch=-2), "batch_size"),
+    (dict(num_fields=-1), "num_fields"),
+    (dict(stride=0), "out_row_stride"),
+    (dict(tables=None), "tables"),
+    (dict(offsets=None), "NULL"),
+    (dict(out=None), "NULL"),
+    (dict(values=None), "NULL"),
+])
+def test_forward_rejects_bad_arguments(pkg, kw, needle):
+    if "tables" not in kw:
+        kw["tables"] = _table(pkg)
+    rc = _forward(pkg, **kw)
+    assert rc == pkg._capi.EINVAL
+    assert needle in pkg._capi.last_error()
+
+
+@pytest.mark.parametrize("tkw,needle", [
+    (dict(data=None), "data is NULL"),
+    (dict(rows=0), "rows"),
+    (dict(dim=0), "dim"),
+    (dict(row_stride=64), "row_stride"),
+    (dict(out_col=64), "outside the output row"),
+    (dict(out_col=-1), "outside the output row"),
+])
+def test_forward_rejects_bad_tables(pkg, tkw, needle):
+    rc = _forward(pkg, tables=_table(pkg, **tkw))
+    assert rc == pkg._capi.EINVAL
+    assert needle in pkg._capi.last_error()
+
+
+def test_forward_zero_sized_calls_are_no_ops(pkg):
+    assert _forward(pkg, batch=0, tables=None, values=None, offsets=None, out=None) == pkg._capi.OK
+    assert _forward(pkg, num_fields=0, tables=None) == pkg._capi.OK
+    assert pkg._capi.last_error() == ""
+
+
+def test_fused_all_slots_rejects_bad_arguments(pkg):
+    c = pkg._capi
+    f = c.lib().cti_ebag_fused_all_slots
+    assert f(1, 1, 1, 1, c.BF16, 1, 4, 28, 0, 10, 5, None) == c.EINVAL
+    assert "emb_dim" in c.last_error()
+    assert f(1, 1, 1, 1, c.BF16, 1, 4, 28, 64, -1, 5, None) == c.EINVAL
+    assert "max_idx" in c.last_error()
+    assert f(1, 1, 1, 1, 3, 1, 4, 28, 64, 10, 5, None) == c.EINVAL
+    assert f(1, None, 1, 1, c.BF16, 1, 4, 28, 64, 10, 5, None) == c.EINVAL
+    assert f(None, 1, 1, 1, c.BF16, 1, 4, 28, 64, 10, 5, None) == c.EINVAL  # values NULL with nnz > 0
+    assert f(None, None, None, None, c.BF16, None, 0, 28, 64, 10, 0, None) == c.OK  # empty batch
+
+
+def test_pack_and_merge_reject_bad_arguments(pkg):
+    c = pkg._capi
+    lib = c.lib()
+    nnz = (ctypes.c_int64 * 1)(-1)
+    ptrs = (ctypes.c_void_p * 1)(16)
+    assert lib.cti_ebag_pack_slots(ptrs, ptrs, nnz, 1, 4, 16, 16, 16, None, None) == c.EINVAL
+    assert lib.cti_ebag_pack_slots(None, ptrs, nnz, 1, 4, 16, 16, 16, None, None) == c.EINVAL
+    assert lib.cti_ebag_pack_slots(ptrs, ptrs, nnz, 0, 4, None, None, None, None, None) == c.OK
+    bs = (ctypes.c_int64 * 33)(*([1] * 33))
+    many = (ctypes.c_void_p * 33)(*([16] * 33))
+    assert lib.cti_ebag_merge_batches(many, many, many, bs, bs, 33, 28, 16, 16, 16, None, None) == c.EUNSUPPORTED
+    assert lib.cti_ebag_merge_batches(many, many, many, bs, bs, 2, 40000, 16, 16, 16, None, None) == c.EUNSUPPORTED
+    neg = (ctypes.c_int64 * 2)(-1, 1)
+    assert lib.cti_ebag_merge_batches(many, many, many, neg, bs, 2, 28, 16, 16, 16, None, None) == c.EINVAL
+
+
+def test_workspace_query(pkg):
+    lib = pkg._capi.lib()
+    assert lib.cti_ebag_workspace_bytes(4096, 28) >= 0
+    assert lib.cti_ebag_workspace_bytes(-1, 28) < 0
+
+
+def test_python_wrappers_validate_before_any_launch(pkg):
+    w = torch.zeros(10, 8)
+    v = torch.zeros(3, dtype=torch.int64)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        pkg.fused_all_slots_embedding(v, v[:1], torch.zeros(5, dtype=torch.int64), w, torch.zeros(4, 8), 4, 8, 9)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        pkg.embedding_bag_pooled(v, torch.zeros(5, dtype=torch.int64), [w])
+    with pytest.raises(ValueError, match="at least one table"):
+        pkg.embedding_bag_pooled(v, torch.zeros(5, dtype=torch.int64), [])
+    with pytest.raises(TypeError):
+        pkg._capi.dtype_code(torch.int8)
+    with pytest.raises(ValueError):
+        pkg._capi.pooling_code("max")

@@ -1,0 +1,271 @@
+"""Pins of the CPU oracle (no GPU): against library routines, closed forms, brute force and the
+committed golden fixtures, plus planted mistakes that those pins must catch."""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as Fn
+
+from _cases import I64_MAX, I64_MIN, random_case
+from oracle import ebag_oracle as orc
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def torch_segment_loop(case, pooling="sum"):
+    """baseline/infer.py:256-263 with torch's library routines (fp32 accumulation)."""
+    pooled = []
+    for f in range(case.F):
+        s, e = int(case.offsets[f * case.B]), int(case.offsets[(f + 1) * case.B])
+        vals = torch.from_numpy(case.values[s:e])
+        local = torch.from_numpy(case.offsets[f * case.B:(f + 1) * case.B + 1] - s)
+        w = torch.from_numpy(orc.decode(case.tables[f], case.tdt).copy())
+        vals = vals.clamp(0, w.shape[0] - 1)
+        emb = Fn.embedding(vals, w)
+        res = torch.segment_reduce(emb, reduce="sum", offsets=local, initial=0)
+        if pooling == "mean":
+            L = (local[1:] - local[:-1]).to(torch.float32)
+            res = torch.where(L[:, None] > 0, res / L.clamp(min=1)[:, None], torch.zeros_like(res))
+        pooled.append(res)
+    return torch.cat(pooled, dim=1).numpy()
+
+
+def torch_embedding_bag_loop(case, pooling="sum"):
+    pooled = []
+    for f in range(case.F):
+        s, e = int(case.offsets[f * case.B]), int(case.offsets[(f + 1) * case.B])
+        w = torch.from_numpy(orc.decode(case.tables[f], case.tdt).copy())
+        vals = torch.from_numpy(case.values[s:e]).clamp(0, w.shape[0] - 1)
+        local = torch.from_numpy(case.offsets[f * case.B:(f + 1) * case.B + 1] - s)
+        pooled.append(Fn.embedding_bag(vals, w, local, mode=pooling, include_last_offset=True))
+    return torch.cat(pooled, dim=1).numpy()
+
+
+def f64_reference(case, pooling="sum"):
+    """fp64 pooling of the decoded rows and the fp32 reassociation bound sum_i |x_i| * L * 2^-24."""
+    cols = []
+    bounds = []
+    for f in range(case.F):
+        w = orc.decode(case.tables[f], case.tdt).astype(np.float64)
+        D = w.shape[1]
+        acc = np.zeros((case.B, D))
+        absacc = np.zeros((case.B, D))
+        for b in range(case.B):
+            s, e = case.offsets[f * case.B + b], case.offsets[f * case.B + b + 1]
+            rows = np.clip(case.values[s:e], 0, w.shape[0] - 1)
+            if e > s:
+                acc[b] = w[rows].sum(axis=0)
+                absacc[b] = np.abs(w[rows]).sum(axis=0) * (e - s) * 2.0 ** -24
+                if pooling == "mean":
+                    acc[b] /= (e - s)
+                    absacc[b] /= (e - s)
+        cols.append(acc)
+        bounds.append(absacc)
+    return np.concatenate(cols, axis=1), np.concatenate(bounds, axis=1)
+
+
+CONFIGS = [
+    dict(F=3, B=17, dims=(64,), V=(300,), tdt="f32"),
+    dict(F=5, B=40, dims=(32, 128, 8), V=(50, 1000), tdt="f32", max_len=40),
+    dict(F=2, B=9, dims=(128,), V=(64,), tdt="bf16"),
+    dict(F=4, B=25, dims=(16, 100), V=(70,), tdt="f16"),
+    dict(F=3, B=12, dims=(512,), V=(20,), tdt="bf16", long_every=5, long_len=300),
+]
+
+
+@pytest.mark.parametrize("cfg", range(len(CONFIGS)))
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_c_and_numpy_restatements_agree_bitwise(cfg, pooling):
+    case = random_case(100 + cfg, **CONFIGS[cfg])
+    for odt in ("f32", "bf16", "f16"):
+        a = orc.pool_c(case.values, case.offsets, case.tables, case.tdt, pooling, odt)
+        b = orc.pool_np(case.values, case.offsets, case.tables, case.tdt, pooling, odt)
+        assert np.array_equal(a, b), (cfg, pooling, odt)
+
+
+@pytest.mark.parametrize("cfg", range(len(CONFIGS)))
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_against_torch_library_routines(cfg, pooling):
+    case = random_case(200 + cfg, **CONFIGS[cfg])
+    got = orc.pool_c(case.values, case.offsets, case.tables, case.tdt, pooling, "f32")
+    ref64, bound = f64_reference(case, pooling)
+    assert np.all(np.abs(got - ref64) <= bound + 1e-30)
+    if pooling == "sum":
+        seg = torch_segment_loop(case, pooling)
+        np.testing.assert_allclose(got, seg, rtol=0, atol=5e-5)
+    eb = torch_embedding_bag_loop(case, pooling)
+    np.testing.assert_allclose(got, eb, rtol=0, atol=5e-5)
+
+
+def test_reference_layout_equals_global_layout():
+    case = random_case(7, F=6, B=31, dims=(64,), V=(400,), tdt="bf16")
+    ro, vo = case.reference_layout()
+    shared = [case.tables[0]] * case.F
+    a = orc.pool_c(case.values, ro, shared, "bf16", "sum", batch=case.B, val_base=vo)
+    b = orc.pool_c(case.values, case.offsets, shared, "bf16", "sum")
+    assert np.array_equal(a, b)
+    g = orc.to_global_offsets(vo, ro, case.B, len(case.values))
+    assert np.array_equal(g, case.offsets)
+
+
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_integer_tables_are_exact(pooling):
+    # integer rows in [-32, 32], bags up to 2048 long: every fp32 partial sum is an exact integer
+    case = random_case(11, F=3, B=20, dims=(64, 128), V=(1000,), tdt="f32", kind="int", max_len=64,
+                       long_every=4, long_len=2048)
+    got = orc.pool_c(case.values, case.offsets, case.tables, "f32", pooling, "f32")
+    for f in range(case.F):
+        w = case.tables[f].astype(np.int64)
+        D = w.shape[1]
+        col = sum(case.tables[g].shape[1] for g in range(f))
+        for b in range(case.B):
+            s, e = case.offsets[f * case.B + b], case.offsets[f * case.B + b + 1]
+            exact = w[np.clip(case.values[s:e], 0, w.shape[0] - 1)].sum(axis=0) if e > s else np.zeros(D, np.int64)
+            want = exact.astype(np.float32)
+            if pooling == "mean" and e > s:
+                want = want / np.float32(e - s)
+            assert np.array_equal(got[b, col:col + D], want), (f, b)
+
+
+def test_rowid_tables_identify_every_row():
+    # table[r, j] = bit j of r: a length-1 bag returns the bits of the row actually read
+    V, D = 5000, 16
+    r = np.arange(V, dtype=np.int64)
+    table = ((r[:, None] >> np.arange(D)) & 1).astype(np.float32)
+    ids = np.array([0, 1, V - 1, V, -1, I64_MAX, I64_MIN, 1234, -(2 ** 40), V + 99], dtype=np.int64)
+    offsets = np.arange(len(ids) + 1, dtype=np.int64)
+    got = orc.pool_c(ids, offsets, [table], "f32", "sum", "f32")
+    rows = np.clip(ids, 0, V - 1)
+    want = ((rows[:, None] >> np.arange(D)) & 1).astype(np.float32)
+    assert np.array_equal(got, want)
+    assert list(rows[3:7]) == [V - 1, 0, V - 1, 0]
+
+
+def test_empty_bags_pool_to_positive_zero():
+    V, D = 10, 8
+    table = np.full((V, D), -3.5, dtype=np.float32)
+    offsets = np.array([0, 0, 2, 2, 2], dtype=np.int64)  # bags: empty, 2 rows, empty, empty
+    ids = np.array([1, 2], dtype=np.int64)
+    for pooling in ("sum", "mean"):
+        for odt in ("f32", "bf16", "f16"):
+            got = orc.pool_c(ids, offsets, [table], "f32", pooling, odt)
+            raw = got.view(np.uint32) if odt == "f32" else got
+            assert np.all(raw[[0, 2, 3]] == 0), (pooling, odt)  # +0 bit pattern
+    got = orc.pool_c(ids, offsets, [table], "f32", "mean", "f32")
+    assert np.all(got[1] == -3.5)
+
+
+def test_brute_force_tiny():
+    # pure-Python scalar loop, fp32 at every step, on tiny inputs
+    for seed in range(5):
+        case = random_case(300 + seed, F=2, B=5, dims=(3, 5), V=(9,), tdt="f32", max_len=6)
+        for pooling in ("sum", "mean"):
+            got = orc.pool_c(case.values, case.offsets, case.tables, "f32", pooling, "f32")
+            col = 0
+            for f in range(case.F):
+                t = case.tables[f]
+                for b in range(case.B):
+                    s, e = int(case.offsets[f * case.B + b]), int(case.offsets[f * case.B + b + 1])
+                    for d in range(t.shape[1]):
+                        acc = np.float32(0.0)
+                        for i in range(s, e):
+                            row = min(max(int(case.values[i]), 0), t.shape[0] - 1)
+                            acc = np.float32(acc + t[row, d])
+                        if pooling == "mean" and e > s:
+                            acc = np.float32(acc / np.float32(e - s))
+                        assert got[b, col + d] == acc
+                col += t.shape[1]
+
+
+def test_bf16_encoder_matches_torch():
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        rng.normal(0, 1, 20000).astype(np.float32),
+        rng.normal(0, 1e-38, 2000).astype(np.float32),                       # subnormals
+        (rng.integers(0, 2 ** 16, 4000, dtype=np.uint32) << 16 | 0x8000).view(np.float32),  # exact ties
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 3.4028235e38, -3.4028235e38, 3.3961776e38], np.float32),
+    ])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    for got in (orc.f32_to_bf16(x), orc.c_f32_to_bf16(x)):
+        fin = ~np.isnan(x)
+        assert np.array_equal(got[fin], want[fin])
+        assert np.all(np.isnan(orc.bf16_to_f32(got[~fin])))
+    # decode is exact: bf16 -> fp32 -> bf16 is the identity on every non-NaN pattern
+    pats = np.arange(2 ** 16, dtype=np.uint32).astype(np.uint16)
+    dec = orc.bf16_to_f32(pats)
+    keep = ~np.isnan(dec)
+    assert np.array_equal(orc.f32_to_bf16(dec)[keep], pats[keep])
+    assert np.array_equal(dec, torch.from_numpy(pats.view(np.int16)).view(torch.bfloat16).float().numpy(),
+                          equal_nan=True)
+
+
+def test_f16_encoder_matches_numpy():
+    rng = np.random.default_rng(6)
+    x = np.concatenate([
+        rng.normal(0, 1, 20000).astype(np.float32),
+        rng.normal(0, 1e-5, 5000).astype(np.float32),       # fp16 subnormal range
+        rng.normal(0, 1e5, 2000).astype(np.float32),        # overflow range
+        (np.arange(-30, 17, dtype=np.float32)[:, None] * 0 + 2.0 ** np.arange(-30, 17)[:, None]
+         * (1 + np.array([2 ** -11, 3 * 2 ** -11], np.float32))).reshape(-1).astype(np.float32),  # ties
+        np.array([0.0, -0.0, np.inf, -np.inf, 65504.0, 65519.996, 65520.0, 2.0 ** -25, 2.0 ** -24], np.float32),
+    ])
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(orc.c_f32_to_f16(x), want)
+    pats = np.arange(2 ** 16, dtype=np.uint32).astype(np.uint16)
+    a = orc.c_f16_to_f32(pats)
+    b = pats.view(np.float16).astype(np.float32)
+    assert np.array_equal(a, b, equal_nan=True)
+
+
+# ---- planted mistakes: each plausible bug in a restatement must fail one of the pins ----------
+def _mutant_no_clamp(values, offsets, tables, tdt, pooling, odt):
+    V = tables[0].shape[0]
+    return orc.pool_c(np.mod(values, V), offsets, tables, tdt, pooling, odt)  # wraps instead of clamps
+
+
+def _mutant_off_by_one(values, offsets, tables, tdt, pooling, odt):
+    o = offsets.copy()
+    o[1:-1] += 1  # bag boundaries shifted by one element
+    return orc.pool_c(values, o, tables, tdt, pooling, odt)
+
+
+def _mutant_swapped_fields(values, offsets, tables, tdt, pooling, odt):
+    t = list(tables)
+    t[0], t[1] = t[1], t[0]
+    return orc.pool_c(values, offsets, t, tdt, pooling, odt)
+
+
+def _mutant_mean_for_sum(values, offsets, tables, tdt, pooling, odt):
+    return orc.pool_c(values, offsets, tables, tdt, "mean" if pooling == "sum" else "sum", odt)
+
+
+@pytest.mark.parametrize("mutant", [_mutant_no_clamp, _mutant_off_by_one, _mutant_swapped_fields, _mutant_mean_for_sum])
+def test_pins_catch_planted_mistakes(mutant):
+    # the integer-table pin (exact closed form) must reject each mutant
+    case = random_case(13, F=2, B=30, dims=(16,), V=(200,), tdt="f32", kind="int", max_len=8, clamp_frac=0.3)
+    good = orc.pool_c(case.values, case.offsets, case.tables, "f32", "sum", "f32")
+    bad = mutant(case.values, case.offsets, case.tables, "f32", "sum", "f32")
+    want = torch_segment_loop(case, "sum")
+    assert np.array_equal(good, want)
+    assert not np.array_equal(bad, want)
+
+
+# ---- golden fixtures --------------------------------------------------------------------------
+def _fixtures():
+    return sorted(glob.glob(os.path.join(GOLDEN, "*.npz")))
+
+
+def test_golden_fixtures_exist():
+    assert len(_fixtures()) >= 5
+
+
+@pytest.mark.parametrize("path", _fixtures(), ids=lambda p: os.path.basename(p))
+def test_oracle_reproduces_golden_fixtures(path):
+    from golden import fixture_io
+
+    fx = fixture_io.load(path)
+    got = orc.pool_c(fx["values"], fx["offsets"], fx["tables"], fx["table_dtype"], fx["pooling"],
+                     fx["out_dtype"], batch=fx["batch"], val_base=fx.get("val_base"))
+    assert np.array_equal(got, fx["expected"])
