@@ -7,10 +7,10 @@ are resident in HBM before timing; step k uses index set k mod n_sets, so consec
 not find each other's rows in L2 / MALL.
 
 Printed (one JSON line): pooled bags/s over the timed steps, plus
-  roofline     algorithmic bytes per launch / mean launch duration (HIP events around every
-               launch on the stream the kernel runs on), against 8 TB/s; `traffic` is the HBM
-               traffic per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary committed
-               under profiles/ (null when absent)
+  roofline     algorithmic bytes per launch / mean launch duration (one pair of HIP events
+               around the K timed launches, on the stream the kernels run on), against 8 TB/s;
+               `traffic` is the HBM traffic per launch from the rocprofv3 FETCH_SIZE /
+               WRITE_SIZE summary committed under profiles/ (null when absent)
   cpu_baseline the reference's CPU pooling loop (F.embedding_bag per field, the oracle's
                restatement) on this host, on a bounded sample of the same batch
 """
@@ -44,13 +44,16 @@ def log(msg):
 
 
 def traffic_from_profiles(workload):
-    """HBM bytes per launch recorded by the rocprofv3 counter runs (profiles/), or None."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    """HBM bytes per launch recorded by the rocprofv3 counter runs, read from the line
+    `hbm_bytes_per_launch: N` of profiles/pool_kernel_<workload>.md, or None."""
+    path = os.path.join(ROOT, "profiles", f"pool_kernel_{workload}.md")
     if not os.path.exists(path):
         return None
     with open(path) as fh:
-        rec = json.load(fh)
-    return rec.get("hbm_bytes_per_launch")
+        for line in fh:
+            if line.strip().startswith("hbm_bytes_per_launch:"):
+                return float(line.split(":", 1)[1].strip())
+    return None
 
 
 def cpu_baseline(wl, tables_dev, seconds):
@@ -99,6 +102,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--long-threshold", type=int, default=0)
+    ap.add_argument("--bins", action="store_true", help="run the device length-binning pass")
+    ap.add_argument("--block-threshold", type=int, default=0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only copy 1 GiB device-to-device 3 times (scales rocprofv3 FETCH/WRITE_SIZE) and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -109,6 +116,17 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.calibrate_copy:
+        n = 1 << 28  # 2^28 fp32 = 1 GiB read + 1 GiB written per copy
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 1 GiB three times")
+        return
 
     from __graft_entry__ import load_package
 
@@ -123,7 +141,8 @@ def main():
     log("filling tables on the device")
     tables = W.make_tables(wl0, dev, seed=0)
     inputs = [W.to_device(wl, dev) for wl in wls]
-    plan = pkg.PooledEmbedding(tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype, long_threshold=args.long_threshold)
+    plan = pkg.PooledEmbedding(tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype, long_threshold=args.long_threshold,
+                               use_bins=args.bins, block_threshold=args.block_threshold, max_batch=wl0.batch)
     out = torch.empty((wl0.batch, sum(wl0.dims)), dtype=wl0.out_dtype, device=dev)
     bytes_alg = [wl.bytes_algorithmic() for wl in wls]
     bytes_comp = [wl.bytes_compulsory() for wl in wls]
@@ -135,29 +154,29 @@ def main():
         plan(v, o, out)
     torch.cuda.synchronize()
 
+    # Timed region: K back-to-back steps, bracketed by one pair of HIP events recorded on the
+    # stream the kernels run on (per-step events would add a gap between kernels).
     K = args.steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     log(f"timing {K} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record()
     for i in range(K):
         v, o = inputs[i % args.sets]
-        starts[i].record()
         plan(v, o, out)
-        ends[i].record()
+    ev1.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    mean_launch_s = float(np.mean(launch_ms)) / 1e3
+    mean_launch_s = ev0.elapsed_time(ev1) / 1e3 / K
     used_bytes = float(np.mean([bytes_alg[i % args.sets] for i in range(K)]))
     used_comp = float(np.mean([bytes_comp[i % args.sets] for i in range(K)]))
     ms_per_step = elapsed / K * 1e3
     value = wl0.num_bags / (elapsed / K)
     achieved = used_bytes / mean_launch_s / 1e9
-    log(f"{ms_per_step * 1e3:.1f} us/step, launch {mean_launch_s * 1e6:.1f} us (median "
-        f"{np.median(launch_ms) * 1e3:.1f}), {achieved:.0f} GB/s algorithmic, "
-        f"{used_comp / mean_launch_s / 1e9:.0f} GB/s compulsory")
+    log(f"{ms_per_step * 1e3:.1f} us/step wall, {mean_launch_s * 1e6:.1f} us/step on the GPU, "
+        f"{achieved:.0f} GB/s algorithmic, {used_comp / mean_launch_s / 1e9:.0f} GB/s compulsory")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -179,12 +198,13 @@ def main():
         "data": f"synthetic: {args.sets} seeded index sets rotated, random N(0, 0.01) tables",
         "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}", "batch": wl0.batch,
                    "fields": wl0.num_fields, "dims": sorted(set(wl0.dims)), "pooling": wl0.pooling,
-                   "nnz_mean": float(np.mean([wl.nnz for wl in wls])), "index_sets": args.sets},
+                   "nnz_mean": float(np.mean([wl.nnz for wl in wls])), "index_sets": args.sets,
+                   "length_binning": bool(args.bins)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profiles(args.workload),
-                     "kernel": "pool_kernel", "bytes_per_launch": used_bytes,
-                     "compulsory_bytes_per_launch": used_comp, "launch_us_mean": mean_launch_s * 1e6,
-                     "launch_us_median": float(np.median(launch_ms)) * 1e3},
+                     "kernel": "pool_kernel" if not args.bins else "bin_kernel + pool_kernel + pool_long_kernel",
+                     "bytes_per_launch": used_bytes,
+                     "compulsory_bytes_per_launch": used_comp, "launch_us_mean": mean_launch_s * 1e6},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -58,7 +58,8 @@ class Options(ctypes.Structure):
     _fields_ = [
         ("long_threshold", ctypes.c_int32),
         ("use_bins", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 6),
+        ("block_threshold", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 5),
     ]
 
 

@@ -3,26 +3,35 @@
 // Semantics follow the reference kernel online_best/infer.py:805-827 and the per-field oracle
 // loop baseline/infer.py:256-263:
 //   out[b, col_f + d] = pool_{i in bag(f, b)} table_f[clamp(values[i], 0, rows_f - 1), d]
-// with fp32 accumulation in element order, empty bag -> 0, and one rounding to the output type.
+// with fp32 accumulation, empty bag -> 0, and one rounding to the output type.
 //
-// Work decomposition (memory-bound gather; no matrix cores):
-//   * A workgroup is 4 wavefronts and owns one tile of consecutive bags of one field.
-//   * A row of D elements is read as 16-byte vectors by LANES = row_bytes/16 lanes; a wavefront
-//     therefore holds R = 64/LANES "subgroups", each pooling one bag. Each lane of a subgroup
-//     accumulates its columns over the bag's rows in order, so a bag pooled this way matches a
-//     sequential fp32 sum bit for bit. For D = 128 bf16: 16 lanes x 16 B per row, 4 bags per
-//     wavefront, 16 bags per workgroup, up to 8 rows in flight per subgroup.
-//   * Bags longer than the split threshold are pooled after the short ones by the whole
-//     workgroup: each wavefront takes a contiguous quarter of the bag, its subgroups take
-//     interleaved rows, partials are combined across subgroups with xor shuffles and across
-//     wavefronts through LDS, always in the same order (results are deterministic).
-//   * Indices are loaded once per subgroup chunk (one lane per index, coalesced) and broadcast
-//     to the subgroup with ds_bpermute; rows are clamped before the address is formed.
-//   * Blocks are renumbered so that each of the 8 XCDs (each with its own L2) works on a
-//     contiguous range of tiles, i.e. on a few fields, which keeps repeated (Zipf-hot) rows of a
-//     field in one L2.
-//   * Shapes whose rows are not whole 16-byte vectors (or misaligned buffers) use an element-wise
-//     kernel with one wavefront per bag.
+// This is a memory-bound gather (no matrix cores). Work decomposition:
+//   * A row of D elements is read as 16-byte vectors by LANES = row_bytes/16 lanes, so a 64-lane
+//     wavefront holds R = 64/LANES lane groups ("subgroups"). For D = 128 bf16: 16 lanes x 16 B
+//     per row, 4 subgroups per wavefront.
+//   * Main kernel: one wavefront per workgroup, one tile of R consecutive bags of one field.
+//       - short bag (L <= sub_threshold): pooled by one subgroup; each lane adds its columns of
+//         the bag's rows in element order, so the result equals a sequential fp32 sum bit for bit;
+//       - medium bag (sub_threshold < L <= block_threshold): split over the wavefront's subgroups
+//         (interleaved rows), partials combined with an xor butterfly in a fixed order;
+//       - long bag (L > block_threshold, only with the length-binning pass): left to the long kernel.
+//     Single-wavefront workgroups need no workgroup barrier, so a wavefront retires as soon as its
+//     own bags are done (measured: 4-wavefront workgroups are ~10% slower on D=128 bf16).
+//     ROWS_IN_FLIGHT row loads per lane are issued before any is consumed.
+//   * Length-binning pass (optional): one thread per bag; bags longer than block_threshold are
+//     appended to a list in the caller's workspace (one atomic per wavefront).
+//   * Long kernel: 8 wavefronts (4 for 2 KB rows) per workgroup, looping over the list; each bag
+//     is cut into one contiguous slice per wavefront, and the wavefront partials are combined
+//     through LDS in wavefront order.
+//   * List counter hand-off without contended atomics: the binning pass counts into `count`; the
+//     main kernel, which runs between the two, has one thread move `count` to `total` and zero
+//     `count`; the long kernel reads `total`. A call therefore leaves `count` at zero for the next.
+//   * Tiles are renumbered so each of the 8 XCDs (own L2 each) works on a contiguous range of
+//     tiles, i.e. on a few fields at a time.
+//   * Rows that are not whole 16-byte vectors, or misaligned buffers, use an element-wise kernel
+//     (one wavefront per bag, element order, never split).
+// All kernels write disjoint output rows and combine partial sums in a fixed order, so results
+// are deterministic run to run.
 #include <stdint.h>
 #include <string.h>
 
@@ -34,9 +43,32 @@
 namespace cti {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWave * kWaves;
+// Tuning knobs (compile-time). Defaults are the measured best on MI355X for D=128 bf16.
+#ifndef CTI_EBAG_ROWS_IN_FLIGHT
+#define CTI_EBAG_ROWS_IN_FLIGHT 4  // 16-byte row loads in flight per lane before they are consumed
+#endif
+#ifndef CTI_EBAG_XCD_REMAP
+#define CTI_EBAG_XCD_REMAP 1  // give each XCD a contiguous range of tiles
+#endif
+#ifndef CTI_EBAG_NT_ROWS
+#define CTI_EBAG_NT_ROWS 0  // non-temporal hint on table-row loads
+#endif
+
+constexpr int kMainThreads = kWave;  // main kernel: one wavefront per workgroup
+constexpr int kBinThreads = 256;
+constexpr int64_t kLongBlocksMax = 1024;  // workgroups of the long kernel (they loop over the list)
 constexpr int kMaxFields = 64;
+constexpr int64_t kNoLimit = INT64_MAX;
+
+__device__ __forceinline__ uint4 load_row16(const char* p) {
+#if CTI_EBAG_NT_ROWS
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return load16(p);
+#endif
+}
 
 enum Variant : int {
   kVarL1 = 0,  // LANES = 1 << v, one 16-byte vector per lane, for v = 0..6
@@ -61,33 +93,42 @@ struct PoolParams {
   const int64_t* offsets;   // bag offsets, field f starts at offsets + gidx * offsets_stride
   const int64_t* val_base;  // optional per-field base added to offsets (reference layout)
   char* out;
-  const int32_t* tile_order;  // optional logical->physical tile map (length-binning pass)
   int64_t nnz;
   int64_t offsets_stride;
-  int64_t out_row_stride;  // elements
+  int64_t out_row_stride;   // elements
   int64_t batch;
+  int64_t sub_threshold;    // longer bags are split over a wavefront's subgroups
+  int64_t block_threshold;  // longer bags go to the long kernel (kNoLimit without binning)
+  unsigned int* bin_count;  // binning: list length being built (NULL without binning)
+  unsigned int* bin_total;  // binning: list length handed to the long kernel
   int32_t num_fields;
   int32_t num_tiles;
-  int32_t pooling;  // CTI_EBAG_SUM / CTI_EBAG_MEAN
-  int32_t long_threshold;
+  int32_t pooling;          // CTI_EBAG_SUM / CTI_EBAG_MEAN
   int32_t idx32;
-  int32_t pad;
   FieldDesc f[kMaxFields];
 };
 
-// The hardware deals workgroups to the 8 XCDs round-robin by id. Renumber so XCD x receives
-// one contiguous range of tiles (a bijection on [0, n)).
+// Workspace of the length-binning pass: counters, then the list of long bags.
+struct LongList {
+  unsigned int* count;  // list length, incremented by the binning pass
+  unsigned int* total;  // list length snapshot read by the long kernel
+  int64_t* bags;        // (local field index << 40) | sample index
+};
+constexpr int64_t kWorkspaceHeader = 256;
+
 __device__ __forceinline__ int xcd_contiguous(int bid, int n) {
+  // Hardware deals workgroups to the 8 XCDs round-robin; map XCD x to one contiguous range.
   const int x = bid & 7, s = bid >> 3;
   const int q = n >> 3, r = n & 7;
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + s;
 }
 
-__device__ __forceinline__ int block_tile(const PoolParams& p) {
-  const int bid = static_cast<int>(blockIdx.x);
-  // With a binned order the list is already ranked heavy-first; deal it round-robin.
-  if (p.tile_order) return p.tile_order[bid];
-  return xcd_contiguous(bid, static_cast<int>(gridDim.x));
+__device__ __forceinline__ int block_tile() {
+#if CTI_EBAG_XCD_REMAP
+  return xcd_contiguous(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+#else
+  return static_cast<int>(blockIdx.x);
+#endif
 }
 
 __device__ __forceinline__ int find_field(const PoolParams& p, int tile) {
@@ -112,22 +153,76 @@ __device__ __forceinline__ void bag_range(const PoolParams& p, int gidx, int64_t
   end = clamp_i64(base + o[1], start, p.nnz);
 }
 
-// Vector kernel: LANES lanes x VPL 16-byte vectors per row.
+// Row shape of one kernel instance.
+template <typename TT, int LANES, int VPL>
+struct Shape {
+  static constexpr int R = kWave / LANES;            // subgroups per wavefront
+  static constexpr int VEC = 16 / Elem<TT>::kBytes;  // elements per 16-byte vector
+  static constexpr int NACC = VPL * VEC;             // fp32 accumulators per lane
+  static constexpr int D = LANES * NACC;             // row width
+  static constexpr int U0 = CTI_EBAG_ROWS_IN_FLIGHT / VPL > 0 ? CTI_EBAG_ROWS_IN_FLIGHT / VPL : 1;
+  static constexpr int U = U0 < LANES ? U0 : LANES;  // rows per subgroup per step
+};
+
+// Accumulate the rows of elements [s0, s1) into this lane's columns; subgroup g of the
+// wavefront takes elements s0 + g, s0 + g + R, ... in order. Wave-uniform s0, s1.
+template <typename TT, int LANES, int VPL>
+__device__ __forceinline__ void wave_slice_partial(const PoolParams& p, const char* table, int64_t max_row,
+                                                   int64_t row_bytes, int64_t s0, int64_t s1, float* pa) {
+  using S = Shape<TT, LANES, VPL>;
+  const int lane = lane_id();
+  const int g = lane / LANES, sl = lane % LANES;
+  for (int64_t c = s0; c < s1; c += kWave) {
+    int64_t roff = 0;
+    if (c + lane < s1) roff = clamp_i64(load_index(p, c + lane), 0, max_row) * row_bytes;
+    const int n = static_cast<int>(s1 - c < kWave ? s1 - c : kWave);
+    for (int k = 0; k < n; k += S::U * S::R) {
+      uint4 v[S::U][VPL];
+#pragma unroll
+      for (int u = 0; u < S::U; ++u) {
+        const int e = k + u * S::R + g;  // < 64 because U * R <= 64
+        const int64_t ro = shfl_i64(roff, e);
+        const bool act = e < n;
+#pragma unroll
+        for (int q = 0; q < VPL; ++q)
+          v[u][q] = act ? load_row16(table + ro + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < S::U; ++u) {
+#pragma unroll
+        for (int q = 0; q < VPL; ++q) acc16(pa + q * S::VEC, v[u][q], TT{});
+      }
+    }
+  }
+  // subgroups -> wavefront: butterfly over the lane bits above the subgroup width
+#pragma unroll
+  for (int mk = LANES; mk < kWave; mk <<= 1) {
+#pragma unroll
+    for (int i = 0; i < S::NACC; ++i) pa[i] += shfl_xor_f32(pa[i], mk);
+  }
+}
+
 template <typename TT, typename OT, int LANES, int VPL>
-__global__ void __launch_bounds__(kThreads) pool_kernel(const PoolParams p) {
-  constexpr int R = kWave / LANES;               // bags per wavefront
-  constexpr int TB = kWaves * R;                 // bags per tile
-  constexpr int VEC = 16 / Elem<TT>::kBytes;     // elements per 16-byte vector
-  constexpr int NACC = VPL * VEC;                // fp32 accumulators per lane
-  constexpr int D = LANES * NACC;                // row width handled by this instance
-  constexpr int U0 = 8 / VPL;                    // rows in flight per subgroup per step
-  constexpr int U = U0 < LANES ? U0 : LANES;
+__device__ __forceinline__ void store_bag(const PoolParams& p, int64_t b, int out_col, int64_t L, float* a) {
+  using S = Shape<TT, LANES, VPL>;
+  const int sl = lane_id() % LANES;
+  if (p.pooling == CTI_EBAG_MEAN && L > 0) {
+    const float fl = static_cast<float>(L);
+#pragma unroll
+    for (int i = 0; i < S::NACC; ++i) a[i] = a[i] / fl;
+  }
+  OT* o = reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col;
+#pragma unroll
+  for (int q = 0; q < VPL; ++q) store_out<S::VEC>(o + (q * LANES + sl) * S::VEC, a + q * S::VEC);
+}
 
-  __shared__ float s_red[kWaves * D];
-  __shared__ int64_t s_start[TB], s_end[TB], s_bag[TB];
-  __shared__ int s_cnt[kWaves];
+// Main kernel: one wavefront, one tile of R bags of one field.
+template <typename TT, typename OT, int LANES, int VPL>
+__global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
+  using S = Shape<TT, LANES, VPL>;
+  constexpr int U = S::U;
 
-  const int tile = block_tile(p);
+  const int tile = block_tile();
   const int fi = find_field(p, tile);
   const char* const table = p.f[fi].table;
   const int64_t max_row = p.f[fi].max_row;
@@ -136,22 +231,29 @@ __global__ void __launch_bounds__(kThreads) pool_kernel(const PoolParams p) {
   const int out_col = p.f[fi].out_col;
 
   const int lane = lane_id();
-  const int wave = static_cast<int>(threadIdx.x) >> 6;
   const int g = lane / LANES;   // subgroup inside the wavefront
   const int sl = lane % LANES;  // lane inside the subgroup
 
-  const int64_t b = static_cast<int64_t>(tile - p.f[fi].tile_begin) * TB + wave * R + g;
+  if (p.bin_count && blockIdx.x == 0 && threadIdx.x == 0) {
+    // hand the finished list length to the long kernel and zero the counter for the next call
+    const unsigned int n = __hip_atomic_load(p.bin_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.bin_total, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.bin_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  const int64_t b = static_cast<int64_t>(tile - p.f[fi].tile_begin) * S::R + g;
   const bool valid = b < p.batch;
   int64_t start = 0, end = 0;
   if (valid) bag_range(p, gidx, b, start, end);
   const int64_t L = end - start;
-  const bool split = valid && L > 0 && L > p.long_threshold;
-  const int64_t Ls = split ? 0 : L;
+  const bool medium = valid && L > p.sub_threshold && L <= p.block_threshold;
+  const bool mine = valid && L <= p.sub_threshold;  // pooled by this subgroup
+  const int64_t Ls = mine ? L : 0;
 
   // ---- short bags: one subgroup per bag, rows accumulated in order -------------------------
-  float acc[NACC];
+  float acc[S::NACC];
 #pragma unroll
-  for (int i = 0; i < NACC; ++i) acc[i] = 0.f;
+  for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
 
   const int64_t maxL = wave_max_i64(Ls);
   for (int64_t c = 0; c < maxL; c += LANES) {
@@ -165,116 +267,98 @@ __global__ void __launch_bounds__(kThreads) pool_kernel(const PoolParams p) {
         const int64_t ro = shfl_i64(roff, g * LANES + k + u);
         const bool act = c + k + u < Ls;
 #pragma unroll
-        for (int q = 0; q < VPL; ++q) {
-          v[u][q] = act ? load16(table + ro + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
-        }
+        for (int q = 0; q < VPL; ++q)
+          v[u][q] = act ? load_row16(table + ro + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
 #pragma unroll
-        for (int q = 0; q < VPL; ++q) acc16(acc + q * VEC, v[u][q], TT{});
+        for (int q = 0; q < VPL; ++q) acc16(acc + q * S::VEC, v[u][q], TT{});
       }
     }
   }
+  if (mine) store_bag<TT, OT, LANES, VPL>(p, b, out_col, L, acc);
 
-  if (valid && !split) {
-    if (p.pooling == CTI_EBAG_MEAN && L > 0) {
-      const float fl = static_cast<float>(L);
+  // ---- medium bags: the whole wavefront on one bag at a time -------------------------------
+  uint64_t m = __ballot(medium && sl == 0);
+  while (m) {
+    const int src = __ffsll(static_cast<long long>(m)) - 1;  // lane 0 of the owning subgroup
+    m &= m - 1;
+    const int64_t bs = shfl_i64(start, src), be = shfl_i64(end, src), bb = shfl_i64(b, src);
+    float pa[S::NACC];
 #pragma unroll
-      for (int i = 0; i < NACC; ++i) acc[i] = acc[i] / fl;
-    }
-    OT* o = reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col;
-#pragma unroll
-    for (int q = 0; q < VPL; ++q) store_out<VEC>(o + (q * LANES + sl) * VEC, acc + q * VEC);
+    for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
+    wave_slice_partial<TT, LANES, VPL>(p, table, max_row, row_bytes, bs, be, pa);
+    if (g == 0) store_bag<TT, OT, LANES, VPL>(p, bb, out_col, be - bs, pa);
   }
+}
 
-  // ---- long bags of this tile: split over the 4 wavefronts ---------------------------------
-  const uint64_t m = __ballot(split && sl == 0);
-  if (lane == 0) s_cnt[wave] = __popcll(m);
-  __syncthreads();
-  int before = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const int cw = s_cnt[w];
-    before += w < wave ? cw : 0;
-    total += cw;
+// Length-binning pass: list the bags longer than block_threshold. grid (ceil(B/256), fields).
+__global__ void __launch_bounds__(kBinThreads) bin_kernel(const PoolParams p, LongList l) {
+  const int fi = static_cast<int>(blockIdx.y);
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * kBinThreads + threadIdx.x;
+  bool is_long = false;
+  if (b < p.batch) {
+    int64_t s, e;
+    bag_range(p, p.f[fi].gidx, b, s, e);
+    is_long = e - s > p.block_threshold;
   }
-  if (total == 0) return;  // uniform over the workgroup
-  if (split && sl == 0) {
-    const int pos = before + __popcll(m & ((1ull << lane) - 1ull));
-    s_start[pos] = start;
-    s_end[pos] = end;
-    s_bag[pos] = b;
+  const uint64_t m = __ballot(is_long);
+  if (m == 0) return;  // uniform over the wavefront
+  const int lane = lane_id();
+  unsigned int base = 0;
+  if (lane == 0) base = atomicAdd(l.count, static_cast<unsigned int>(__popcll(m)));
+  base = static_cast<unsigned int>(shfl_i32(static_cast<int>(base), 0));
+  if (is_long) {
+    const unsigned int pos = base + static_cast<unsigned int>(__popcll(m & ((1ull << lane) - 1ull)));
+    l.bags[pos] = (static_cast<int64_t>(fi) << 40) | b;
   }
-  __syncthreads();
+}
 
-  for (int j = 0; j < total; ++j) {
-    const int64_t bs = s_start[j], be = s_end[j], bb = s_bag[j];
-    const int64_t per = (be - bs + kWaves - 1) / kWaves;
+// Long kernel: LW wavefronts per workgroup; every listed bag is split into LW contiguous slices.
+template <typename TT, typename OT, int LANES, int VPL, int LW>
+__global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams p, LongList l) {
+  using S = Shape<TT, LANES, VPL>;
+  __shared__ float s_red[LW * S::D];
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int g = lane / LANES, sl = lane % LANES;
+  const unsigned int n = __hip_atomic_load(l.total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (unsigned int j = blockIdx.x; j < n; j += gridDim.x) {
+    const int64_t item = l.bags[j];
+    const int fi = static_cast<int>(item >> 40);
+    const int64_t b = item & ((int64_t{1} << 40) - 1);
+    int64_t bs, be;
+    bag_range(p, p.f[fi].gidx, b, bs, be);
+    const int64_t per = (be - bs + LW - 1) / LW;
     const int64_t s0 = bs + wave * per < be ? bs + wave * per : be;
     const int64_t s1 = s0 + per < be ? s0 + per : be;
-
-    float pa[NACC];
+    float pa[S::NACC];
 #pragma unroll
-    for (int i = 0; i < NACC; ++i) pa[i] = 0.f;
-    for (int64_t c = s0; c < s1; c += kWave) {
-      int64_t roff = 0;
-      if (c + lane < s1) roff = clamp_i64(load_index(p, c + lane), 0, max_row) * row_bytes;
-      const int n = static_cast<int>(s1 - c < kWave ? s1 - c : kWave);
-      for (int k = 0; k < n; k += U * R) {
-        uint4 v[U][VPL];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int e = k + u * R + g;  // < 64 because U * R <= 64
-          const int64_t ro = shfl_i64(roff, e);
-          const bool act = e < n;
-#pragma unroll
-          for (int q = 0; q < VPL; ++q) {
-            v[u][q] = act ? load16(table + ro + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-          for (int q = 0; q < VPL; ++q) acc16(pa + q * VEC, v[u][q], TT{});
-        }
-      }
-    }
-    // subgroups -> wavefront: butterfly over the lane bits above the subgroup width
-#pragma unroll
-    for (int mk = LANES; mk < kWave; mk <<= 1) {
-#pragma unroll
-      for (int i = 0; i < NACC; ++i) pa[i] += shfl_xor_f32(pa[i], mk);
-    }
+    for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
+    wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].max_row, p.f[fi].row_bytes, s0, s1, pa);
     if (g == 0) {
 #pragma unroll
       for (int q = 0; q < VPL; ++q) {
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) s_red[wave * D + (q * LANES + sl) * VEC + i] = pa[q * VEC + i];
+        for (int i = 0; i < S::VEC; ++i) s_red[wave * S::D + (q * LANES + sl) * S::VEC + i] = pa[q * S::VEC + i];
       }
     }
     __syncthreads();
     if (wave == 0 && g == 0) {
-      float r[NACC];
+      float r[S::NACC];
 #pragma unroll
       for (int q = 0; q < VPL; ++q) {
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-          const int col = (q * LANES + sl) * VEC + i;
+        for (int i = 0; i < S::VEC; ++i) {
+          const int col = (q * LANES + sl) * S::VEC + i;
           float x = s_red[col];
 #pragma unroll
-          for (int w = 1; w < kWaves; ++w) x += s_red[w * D + col];
-          r[q * VEC + i] = x;
+          for (int w = 1; w < LW; ++w) x += s_red[w * S::D + col];
+          r[q * S::VEC + i] = x;
         }
       }
-      if (p.pooling == CTI_EBAG_MEAN) {
-        const float fl = static_cast<float>(be - bs);
-#pragma unroll
-        for (int i = 0; i < NACC; ++i) r[i] = r[i] / fl;
-      }
-      OT* o = reinterpret_cast<OT*>(p.out) + bb * p.out_row_stride + out_col;
-#pragma unroll
-      for (int q = 0; q < VPL; ++q) store_out<VEC>(o + (q * LANES + sl) * VEC, r + q * VEC);
+      store_bag<TT, OT, LANES, VPL>(p, b, p.f[fi].out_col, be - bs, r);
     }
     __syncthreads();
   }
@@ -283,9 +367,9 @@ __global__ void __launch_bounds__(kThreads) pool_kernel(const PoolParams p) {
 // Element-wise kernel for any row width / alignment: one wavefront per bag, rows accumulated in
 // order, 4 columns per lane per pass.
 template <typename TT, typename OT>
-__global__ void __launch_bounds__(kThreads) pool_generic_kernel(const PoolParams p) {
+__global__ void __launch_bounds__(kMainThreads) pool_generic_kernel(const PoolParams p) {
   constexpr int NC = 4;
-  const int tile = block_tile(p);
+  const int tile = block_tile();
   const int fi = find_field(p, tile);
   const char* const table = p.f[fi].table;
   const int64_t max_row = p.f[fi].max_row;
@@ -293,9 +377,8 @@ __global__ void __launch_bounds__(kThreads) pool_generic_kernel(const PoolParams
   const int dim = p.f[fi].dim;
   const int out_col = p.f[fi].out_col;
   const int lane = lane_id();
-  const int wave = static_cast<int>(threadIdx.x) >> 6;
-  const int64_t b = static_cast<int64_t>(tile - p.f[fi].tile_begin) * kWaves + wave;
-  if (b >= p.batch) return;  // uniform over the wavefront; this kernel has no block barriers
+  const int64_t b = static_cast<int64_t>(tile - p.f[fi].tile_begin);
+  if (b >= p.batch) return;
   int64_t start, end;
   bag_range(p, p.f[fi].gidx, b, start, end);
   const int64_t L = end - start;
@@ -333,16 +416,19 @@ __global__ void __launch_bounds__(kThreads) pool_generic_kernel(const PoolParams
 // Host side
 // ---------------------------------------------------------------------------------------------
 int lanes_of(int variant) { return variant <= 6 ? (1 << variant) : 64; }
-int bags_per_tile(int variant) { return variant == kVarGeneric ? kWaves : kWaves * (kWave / lanes_of(variant)); }
+int bags_per_tile(int variant) { return variant == kVarGeneric ? 1 : kWave / lanes_of(variant); }
 
-int default_long_threshold(int variant) {
-  if (variant == kVarGeneric) return INT32_MAX;  // the element-wise kernel never splits
-  const int lanes = lanes_of(variant);
-  int t = 4 * lanes;
-  if (t < 16) t = 16;
-  if (t > 256) t = 256;
-  return t;
+#ifndef CTI_EBAG_SUB_THRESHOLD
+#define CTI_EBAG_SUB_THRESHOLD 48  // default: longer bags are split over the wavefront's subgroups
+#endif
+
+int64_t default_sub_threshold(int variant) {
+  if (variant == kVarGeneric) return kNoLimit;  // the element-wise kernel never splits
+  return CTI_EBAG_SUB_THRESHOLD;
 }
+
+// With binning, bags longer than this go to the long kernel.
+constexpr int64_t kDefaultBlockThreshold = 512;
 
 int pick_variant(const cti_ebag_table& t, int tb, int ob, const void* out, int64_t out_row_stride) {
   const int64_t row_bytes = static_cast<int64_t>(t.dim) * tb;
@@ -362,35 +448,54 @@ int pick_variant(const cti_ebag_table& t, int tb, int ob, const void* out, int64
   return kVarGeneric;
 }
 
+template <typename TT, typename OT, int LANES, int VPL>
+void launch_shape(const PoolParams& p, const LongList* l, hipStream_t s) {
+  if (l) {
+    const dim3 bgrid(static_cast<unsigned>((p.batch + kBinThreads - 1) / kBinThreads), static_cast<unsigned>(p.num_fields));
+    hipLaunchKernelGGL(bin_kernel, bgrid, dim3(kBinThreads), 0, s, p, *l);
+  }
+  hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL>), dim3(static_cast<unsigned>(p.num_tiles)), dim3(kMainThreads), 0, s, p);
+  if (l) {
+    constexpr int LW = VPL >= 4 ? 4 : 8;  // keeps the LDS partials at <= 32 KB
+    // at most min(bags, nnz / (block_threshold + 1)) bags can be listed
+    int64_t most = p.nnz / (p.block_threshold + 1) + 1;
+    const int64_t bags = p.batch * p.num_fields;
+    if (most > bags) most = bags;
+    const unsigned blocks = static_cast<unsigned>(most < kLongBlocksMax ? (most > 0 ? most : 1) : kLongBlocksMax);
+    hipLaunchKernelGGL((pool_long_kernel<TT, OT, LANES, VPL, LW>), dim3(blocks), dim3(LW * kWave), 0, s, p, *l);
+  }
+}
+
 template <typename TT, typename OT>
-hipError_t launch_variant(int variant, const PoolParams& p, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(p.num_tiles)), block(kThreads);
+hipError_t launch_variant(int variant, const PoolParams& p, const LongList* l, hipStream_t s) {
   switch (variant) {
-    case 0: hipLaunchKernelGGL((pool_kernel<TT, OT, 1, 1>), grid, block, 0, s, p); break;
-    case 1: hipLaunchKernelGGL((pool_kernel<TT, OT, 2, 1>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((pool_kernel<TT, OT, 4, 1>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((pool_kernel<TT, OT, 8, 1>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((pool_kernel<TT, OT, 16, 1>), grid, block, 0, s, p); break;
-    case 5: hipLaunchKernelGGL((pool_kernel<TT, OT, 32, 1>), grid, block, 0, s, p); break;
-    case 6: hipLaunchKernelGGL((pool_kernel<TT, OT, 64, 1>), grid, block, 0, s, p); break;
-    case kVarL64V2: hipLaunchKernelGGL((pool_kernel<TT, OT, 64, 2>), grid, block, 0, s, p); break;
-    case kVarL64V4: hipLaunchKernelGGL((pool_kernel<TT, OT, 64, 4>), grid, block, 0, s, p); break;
-    default: hipLaunchKernelGGL((pool_generic_kernel<TT, OT>), grid, block, 0, s, p); break;
+    case 0: launch_shape<TT, OT, 1, 1>(p, l, s); break;
+    case 1: launch_shape<TT, OT, 2, 1>(p, l, s); break;
+    case 2: launch_shape<TT, OT, 4, 1>(p, l, s); break;
+    case 3: launch_shape<TT, OT, 8, 1>(p, l, s); break;
+    case 4: launch_shape<TT, OT, 16, 1>(p, l, s); break;
+    case 5: launch_shape<TT, OT, 32, 1>(p, l, s); break;
+    case 6: launch_shape<TT, OT, 64, 1>(p, l, s); break;
+    case kVarL64V2: launch_shape<TT, OT, 64, 2>(p, l, s); break;
+    case kVarL64V4: launch_shape<TT, OT, 64, 4>(p, l, s); break;
+    default:
+      hipLaunchKernelGGL((pool_generic_kernel<TT, OT>), dim3(static_cast<unsigned>(p.num_tiles)), dim3(kMainThreads), 0, s, p);
+      break;
   }
   return hipGetLastError();
 }
 
-hipError_t launch_typed(int tdt, int odt, int variant, const PoolParams& p, hipStream_t s) {
+hipError_t launch_typed(int tdt, int odt, int variant, const PoolParams& p, const LongList* l, hipStream_t s) {
   switch (tdt * 3 + odt) {
-    case CTI_EBAG_F32 * 3 + CTI_EBAG_F32: return launch_variant<float, float>(variant, p, s);
-    case CTI_EBAG_F32 * 3 + CTI_EBAG_BF16: return launch_variant<float, bf16_t>(variant, p, s);
-    case CTI_EBAG_F32 * 3 + CTI_EBAG_F16: return launch_variant<float, f16_t>(variant, p, s);
-    case CTI_EBAG_BF16 * 3 + CTI_EBAG_F32: return launch_variant<bf16_t, float>(variant, p, s);
-    case CTI_EBAG_BF16 * 3 + CTI_EBAG_BF16: return launch_variant<bf16_t, bf16_t>(variant, p, s);
-    case CTI_EBAG_BF16 * 3 + CTI_EBAG_F16: return launch_variant<bf16_t, f16_t>(variant, p, s);
-    case CTI_EBAG_F16 * 3 + CTI_EBAG_F32: return launch_variant<f16_t, float>(variant, p, s);
-    case CTI_EBAG_F16 * 3 + CTI_EBAG_BF16: return launch_variant<f16_t, bf16_t>(variant, p, s);
-    default: return launch_variant<f16_t, f16_t>(variant, p, s);
+    case CTI_EBAG_F32 * 3 + CTI_EBAG_F32: return launch_variant<float, float>(variant, p, l, s);
+    case CTI_EBAG_F32 * 3 + CTI_EBAG_BF16: return launch_variant<float, bf16_t>(variant, p, l, s);
+    case CTI_EBAG_F32 * 3 + CTI_EBAG_F16: return launch_variant<float, f16_t>(variant, p, l, s);
+    case CTI_EBAG_BF16 * 3 + CTI_EBAG_F32: return launch_variant<bf16_t, float>(variant, p, l, s);
+    case CTI_EBAG_BF16 * 3 + CTI_EBAG_BF16: return launch_variant<bf16_t, bf16_t>(variant, p, l, s);
+    case CTI_EBAG_BF16 * 3 + CTI_EBAG_F16: return launch_variant<bf16_t, f16_t>(variant, p, l, s);
+    case CTI_EBAG_F16 * 3 + CTI_EBAG_F32: return launch_variant<f16_t, float>(variant, p, l, s);
+    case CTI_EBAG_F16 * 3 + CTI_EBAG_BF16: return launch_variant<f16_t, bf16_t>(variant, p, l, s);
+    default: return launch_variant<f16_t, f16_t>(variant, p, l, s);
   }
 }
 
@@ -409,7 +514,10 @@ struct Job {
   void* out;
   int32_t odt;
   int64_t out_row_stride;
-  int32_t long_threshold;  // 0 = per-variant default
+  int32_t sub_threshold;    // 0 = default, < 0 = split every non-empty bag
+  int32_t use_bins;
+  int32_t block_threshold;  // 0 = default (with bins)
+  void* workspace;
 };
 
 int validate_tables(const Job& j) {
@@ -429,7 +537,15 @@ int validate_tables(const Job& j) {
 int run_job(const Job& j, hipStream_t stream) {
   if (j.batch == 0 || j.num_fields == 0) return CTI_EBAG_OK;
   const int tb = dtype_bytes(j.tdt), ob = dtype_bytes(j.odt);
-  // Group fields by kernel variant; each group is one launch (per 64 fields).
+  LongList list;
+  if (j.use_bins) {
+    if (!j.workspace) return set_error(CTI_EBAG_EWORKSPACE, "length binning requested without a workspace");
+    char* ws = static_cast<char*>(j.workspace);
+    list.count = reinterpret_cast<unsigned int*>(ws);
+    list.total = reinterpret_cast<unsigned int*>(ws) + 1;
+    list.bags = reinterpret_cast<int64_t*>(ws + kWorkspaceHeader);
+  }
+  // Group fields by kernel variant; each group is one launch sequence (per 64 fields).
   std::vector<int> var(j.num_fields);
   for (int f = 0; f < j.num_fields; ++f) var[f] = pick_variant(j.tables[f], tb, ob, j.out, j.out_row_stride);
   for (int v = 0; v < kNumVariants; ++v) {
@@ -442,15 +558,19 @@ int run_job(const Job& j, hipStream_t stream) {
       p.offsets = j.offsets;
       p.val_base = j.val_base;
       p.out = static_cast<char*>(j.out);
-      p.tile_order = nullptr;
       p.nnz = j.nnz;
       p.offsets_stride = j.offsets_stride;
       p.out_row_stride = j.out_row_stride;
       p.batch = j.batch;
       p.pooling = j.pooling;
       p.idx32 = j.idx32;
-      p.long_threshold = j.long_threshold == 0 ? default_long_threshold(v)
-                                               : (j.long_threshold < 0 ? -1 : j.long_threshold);
+      if (v == kVarGeneric) p.sub_threshold = kNoLimit;
+      else if (j.sub_threshold == 0) p.sub_threshold = default_sub_threshold(v);
+      else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;
+      const bool bins = j.use_bins && v != kVarGeneric;
+      p.block_threshold = !bins ? kNoLimit : (j.block_threshold > 0 ? j.block_threshold : kDefaultBlockThreshold);
+      p.bin_count = bins ? list.count : nullptr;
+      p.bin_total = bins ? list.total : nullptr;
       const int bpt = bags_per_tile(v);
       const int64_t tiles_per_field = (j.batch + bpt - 1) / bpt;
       const size_t nf = fields.size() - c0 < static_cast<size_t>(kMaxFields) ? fields.size() - c0 : kMaxFields;
@@ -470,7 +590,7 @@ int run_job(const Job& j, hipStream_t stream) {
         d.tile_begin = static_cast<int32_t>(tiles_per_field * static_cast<int64_t>(i));
       }
       p.num_tiles = static_cast<int32_t>(tiles_per_field * static_cast<int64_t>(nf));
-      const hipError_t e = launch_typed(j.tdt, j.odt, v, p, stream);
+      const hipError_t e = launch_typed(j.tdt, j.odt, v, p, bins ? &list : nullptr, stream);
       if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "pooling kernel launch failed: %s", hipGetErrorString(e));
     }
   }
@@ -478,6 +598,11 @@ int run_job(const Job& j, hipStream_t stream) {
 }
 
 bool dtype_ok(int32_t dt) { return dt == CTI_EBAG_F32 || dt == CTI_EBAG_BF16 || dt == CTI_EBAG_F16; }
+
+int64_t workspace_bytes(int64_t batch, int32_t num_fields) {
+  const int64_t per_launch = num_fields < kMaxFields ? num_fields : kMaxFields;
+  return kWorkspaceHeader + 8 * batch * per_launch;
+}
 
 }  // namespace
 }  // namespace cti
@@ -507,8 +632,8 @@ extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* va
     tables[s].out_col = s * emb_dim;
   }
   Job j;
+  memset(&j, 0, sizeof(j));
   j.values = values;
-  j.idx32 = 0;
   j.nnz = nnz;
   j.offsets = row_offsets;
   j.val_base = val_offsets;
@@ -521,23 +646,20 @@ extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* va
   j.out = out;
   j.odt = dtype;
   j.out_row_stride = static_cast<int64_t>(num_slots) * emb_dim;
-  j.long_threshold = 0;
   return run_job(j, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fields) {
   if (batch_size < 0 || num_fields < 0) return -1;
-  return 0;
+  return workspace_bytes(batch_size, num_fields);
 }
 
 extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
                                 int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables,
                                 int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
-                                int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                                int64_t out_row_stride, void* workspace, int64_t workspace_bytes_given,
                                 const cti_ebag_options* opts, void* stream) {
   clear_error();
-  (void)workspace;
-  (void)workspace_bytes;
   if (index_type != CTI_EBAG_I64 && index_type != CTI_EBAG_I32)
     return set_error(CTI_EBAG_EINVAL, "unknown index type code %d", index_type);
   if (!dtype_ok(table_dtype)) return set_error(CTI_EBAG_EINVAL, "unknown table dtype code %d", table_dtype);
@@ -550,8 +672,9 @@ extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t 
   if (batch_size == 0 || num_fields == 0) return CTI_EBAG_OK;
   if (!tables) return set_error(CTI_EBAG_EINVAL, "tables (host array) is NULL");
   if (!offsets || !out || (nnz > 0 && !values)) return set_error(CTI_EBAG_EINVAL, "NULL device pointer among values/offsets/out");
-  if (opts && opts->use_bins) return set_error(CTI_EBAG_EUNSUPPORTED, "length binning is not available in this build");
+  if (batch_size >= (int64_t{1} << 40)) return set_error(CTI_EBAG_EUNSUPPORTED, "batch_size must be < 2^40");
   Job j;
+  memset(&j, 0, sizeof(j));
   j.values = values;
   j.idx32 = index_type == CTI_EBAG_I32;
   j.nnz = nnz;
@@ -566,7 +689,20 @@ extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t 
   j.out = out;
   j.odt = out_dtype;
   j.out_row_stride = out_row_stride;
-  j.long_threshold = opts ? opts->long_threshold : 0;
+  j.workspace = workspace;
+  if (opts) {
+    j.sub_threshold = opts->long_threshold;
+    j.use_bins = opts->use_bins != 0;
+    j.block_threshold = opts->block_threshold;
+  }
+  if (j.use_bins) {
+    const int64_t need = workspace_bytes(batch_size, num_fields);
+    if (!workspace || workspace_bytes_given < need)
+      return set_error(CTI_EBAG_EWORKSPACE, "length binning needs a zero-initialised workspace of %lld bytes (got %lld)",
+                       (long long)need, (long long)(workspace ? workspace_bytes_given : 0));
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+      return set_error(CTI_EBAG_EINVAL, "workspace must be 256-byte aligned");
+  }
   const int rc = validate_tables(j);
   if (rc != CTI_EBAG_OK) return rc;
   return run_job(j, static_cast<hipStream_t>(stream));

@@ -127,6 +127,8 @@ def embedding_bag_pooled(
     out_dtype: Optional[torch.dtype] = None,
     out: Optional[torch.Tensor] = None,
     long_threshold: int = 0,
+    use_bins: bool = False,
+    block_threshold: int = 0,
 ) -> torch.Tensor:
     """Pool F fields with per-field tables into ``out[B, sum(D_f)]``.
 
@@ -137,8 +139,12 @@ def embedding_bag_pooled(
       pooling  'sum' or 'mean' (mean of an empty bag is 0)
       out_dtype defaults to the tables' dtype; ``out`` (if given) must be contiguous
                [B, sum(D_f)] of that dtype.
-      long_threshold  bags longer than this are split across a workgroup's 4 wavefronts
+      long_threshold  bags longer than this are split over the lane groups of a wavefront
                (0 = per-shape default, -1 = split every non-empty bag).
+      use_bins  run the device length-binning pass: bags longer than ``block_threshold``
+               (0 = default 512) are pooled by a kernel that splits each across the
+               wavefronts of a workgroup. A workspace is allocated for the call; use
+               ``PooledEmbedding`` to keep one across calls.
     Equivalent to, per field, F.embedding_bag(clamp(values_f, 0, V_f-1), table_f, offsets_f,
     mode=pooling) followed by concatenation along dim 1 (baseline/infer.py:256-263).
     """
@@ -189,14 +195,20 @@ def embedding_bag_pooled(
         col += dims[i]
     opts = _capi.Options()
     opts.long_threshold = int(long_threshold)
-    opts.use_bins = 0
+    opts.use_bins = int(bool(use_bins))
+    opts.block_threshold = int(block_threshold)
     lib = _capi.lib()
+    ws, ws_bytes = None, 0
+    if use_bins:
+        ws_bytes = lib.cti_ebag_workspace_bytes(batch_size, num_fields)
+        ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         stream = _capi.current_stream_handle(dev)
         _capi.check(lib.cti_ebag_forward(
             values.data_ptr(), _capi.index_code(values.dtype), values.numel(), offsets.data_ptr(),
             batch_size, num_fields, descs, _capi.dtype_code(tdt), _capi.pooling_code(pooling),
-            out.data_ptr(), _capi.dtype_code(odt), width, None, 0, ctypes.byref(opts), stream))
+            out.data_ptr(), _capi.dtype_code(odt), width, ws.data_ptr() if ws is not None else None, ws_bytes,
+            ctypes.byref(opts), stream))
     return out
 
 
@@ -205,10 +217,13 @@ class PooledEmbedding:
     options are built once, so each call costs one C-ABI call (a few microseconds on the host).
 
     ``plan(values, offsets, out=None)`` pools one batch exactly as embedding_bag_pooled would.
+    With ``use_bins`` the plan owns one workspace, sized for ``max_batch`` samples, whose list
+    counter every call leaves at zero (calls on one plan must not overlap).
     """
 
     def __init__(self, tables: Sequence[torch.Tensor], pooling: str = "sum",
-                 out_dtype: Optional[torch.dtype] = None, long_threshold: int = 0):
+                 out_dtype: Optional[torch.dtype] = None, long_threshold: int = 0,
+                 use_bins: bool = False, block_threshold: int = 0, max_batch: int = 0):
         if len(tables) == 0:
             raise ValueError("at least one table is required")
         self.tables = list(tables)
@@ -233,8 +248,16 @@ class PooledEmbedding:
             col += int(t.shape[1])
         self._opts = _capi.Options()
         self._opts.long_threshold = int(long_threshold)
+        self._opts.use_bins = int(bool(use_bins))
+        self._opts.block_threshold = int(block_threshold)
         self._lib = _capi.lib()
         self._fn = self._lib.cti_ebag_forward
+        self._ws, self._ws_bytes, self.max_batch = None, 0, int(max_batch)
+        if use_bins:
+            if self.max_batch <= 0:
+                raise ValueError("use_bins needs max_batch (the largest batch the plan will see)")
+            self._ws_bytes = self._lib.cti_ebag_workspace_bytes(self.max_batch, self.num_fields)
+            self._ws = torch.zeros(self._ws_bytes, dtype=torch.uint8, device=self.device)
 
     def __call__(self, values: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         if values.device != self.device or offsets.device != self.device:
@@ -250,8 +273,11 @@ class PooledEmbedding:
         elif out.dtype != self.out_dtype or tuple(out.shape) != (batch, self.width) or not out.is_contiguous() \
                 or out.device != self.device:
             raise ValueError(f"out must be a contiguous ({batch}, {self.width}) {self.out_dtype} tensor on {self.device}")
+        if self._ws is not None and batch > self.max_batch:
+            raise ValueError(f"batch {batch} exceeds the plan's max_batch {self.max_batch}")
         stream = torch.cuda.current_stream(self.device).cuda_stream
         _capi.check(self._fn(values.data_ptr(), _capi.index_code(values.dtype), values.numel(), offsets.data_ptr(),
                              batch, self.num_fields, self._descs, self._tdt, self._pool, out.data_ptr(), self._odt,
-                             self.width, None, 0, self._opts, stream))
+                             self.width, self._ws.data_ptr() if self._ws is not None else None, self._ws_bytes,
+                             self._opts, stream))
         return out

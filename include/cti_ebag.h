@@ -74,16 +74,21 @@ typedef struct cti_ebag_table {
   int32_t out_col;
 } cti_ebag_table;
 
-/* Tuning knobs of one launch. Zero-initialise and set only what you need:
- *   long_threshold: bags longer than this are split across the 4 wavefronts of a workgroup
- *                   (partial sums combined through LDS in a fixed order). 0 = default.
- *                   A negative value splits every non-empty bag (used by tests).
- *   use_bins:       1 = run the device length-binning pass and visit heavy tiles first;
- *                   needs a workspace of cti_ebag_workspace_bytes() bytes. 0 = natural order.  */
+/* Tuning knobs of one call. Zero-initialise and set only what you need:
+ *   long_threshold:  bags longer than this are not pooled by one lane group but split over all
+ *                    lane groups of a wavefront (partials combined in a fixed order).
+ *                    0 = default; a negative value splits every non-empty bag (used by tests).
+ *   use_bins:        1 = run the device length-binning pass first: bags longer than
+ *                    block_threshold are listed in the workspace and pooled by a second kernel
+ *                    that splits each of them across the wavefronts of a workgroup (partials
+ *                    combined through LDS in wavefront order). Needs the workspace.
+ *   block_threshold: with use_bins, the length above which a bag goes to that kernel
+ *                    (0 = default, 512).                                                        */
 typedef struct cti_ebag_options {
   int32_t long_threshold;
   int32_t use_bins;
-  int32_t reserved[6];
+  int32_t block_threshold;
+  int32_t reserved[5];
 } cti_ebag_options;
 
 /* ABI version this library was built with (CTI_EBAG_ABI_VERSION). */
@@ -120,8 +125,10 @@ int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* val_offsets,
  *   pooling       CTI_EBAG_SUM or CTI_EBAG_MEAN (mean of an empty bag is 0)
  *   out           [B, out_row_stride] of `out_dtype`; field f writes columns
  *                 [out_col_f, out_col_f + dim_f)
- *   workspace     device scratch of at least cti_ebag_workspace_bytes(...) bytes when
- *                 opts->use_bins is set (else may be NULL); contents need no initialisation
+ *   workspace     device scratch of at least cti_ebag_workspace_bytes(...) bytes, 256-byte
+ *                 aligned, when opts->use_bins is set (else may be NULL). Its first 4 bytes (the
+ *                 list counter) must be zero before the first use; every call leaves them zero
+ *                 again, so one workspace serves any number of calls, one call at a time.
  *   opts          host pointer, may be NULL (all defaults)
  * Replaces the per-field loop at baseline/infer.py:256-263 and generalises the reference
  * kernel (online_best/infer.py:805-827) to per-field tables and mean pooling.
@@ -132,7 +139,8 @@ int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const 
                      int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
                      const cti_ebag_options* opts, void* stream);
 
-/* Bytes of device workspace cti_ebag_forward needs with opts->use_bins = 1. */
+/* Bytes of device workspace cti_ebag_forward needs with opts->use_bins = 1
+ * (256 + 8 * batch_size * min(num_fields, 64)); -1 for negative arguments. */
 int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fields);
 
 /*

@@ -140,8 +140,21 @@ def test_pack_and_merge_reject_bad_arguments(pkg):
 
 def test_workspace_query(pkg):
     lib = pkg._capi.lib()
-    assert lib.cti_ebag_workspace_bytes(4096, 28) >= 0
+    assert lib.cti_ebag_workspace_bytes(4096, 28) == 256 + 8 * 4096 * 28
+    assert lib.cti_ebag_workspace_bytes(10, 100) == 256 + 8 * 10 * 64
     assert lib.cti_ebag_workspace_bytes(-1, 28) < 0
+
+
+def test_binning_requires_a_workspace(pkg):
+    c = pkg._capi
+    opts = c.Options()
+    opts.use_bins = 1
+    rc = _forward(pkg, tables=_table(pkg), opts=ctypes.byref(opts))
+    assert rc == c.EWORKSPACE and "workspace" in c.last_error()
+    rc = _forward(pkg, tables=_table(pkg), opts=ctypes.byref(opts), ws=256, ws_bytes=100)
+    assert rc == c.EWORKSPACE
+    rc = _forward(pkg, tables=_table(pkg), opts=ctypes.byref(opts), ws=8, ws_bytes=1 << 20)
+    assert rc == c.EINVAL and "aligned" in c.last_error()
 
 
 def test_python_wrappers_validate_before_any_launch(pkg):
