@@ -17,7 +17,9 @@
 //       - long bag (L > block_threshold, only with the length-binning pass): left to the long kernel.
 //     Single-wavefront workgroups need no workgroup barrier, so a wavefront retires as soon as its
 //     own bags are done (measured: 4-wavefront workgroups are ~10% slower on D=128 bf16).
-//     ROWS_IN_FLIGHT row loads per lane are issued before any is consumed.
+//     ROWS_IN_FLIGHT row loads per lane are issued before any is consumed. Row ids are clamped,
+//     narrowed to 32 bits (tables have < 2^31 rows) and broadcast to the lanes that read the row
+//     through LDS (one immediate-offset read per row instead of a lane shuffle per row).
 //   * Length-binning pass (optional): one thread per bag; bags longer than block_threshold are
 //     appended to a list in the caller's workspace (one atomic per wavefront).
 //   * Long kernel: 8 wavefronts (4 for 2 KB rows) per workgroup, looping over the list; each bag
@@ -85,7 +87,7 @@ struct FieldDesc {
   int32_t dim;         // columns pooled
   int32_t out_col;     // first output column
   int32_t gidx;        // field index used for offsets / val_base
-  int32_t tile_begin;  // first tile of the field inside this launch
+  int32_t pad;
 };
 
 struct PoolParams {
@@ -103,8 +105,10 @@ struct PoolParams {
   unsigned int* bin_total;  // binning: list length handed to the long kernel
   int32_t num_fields;
   int32_t num_tiles;
+  int32_t tiles_per_field;  // every field of a launch has the same number of tiles
   int32_t pooling;          // CTI_EBAG_SUM / CTI_EBAG_MEAN
   int32_t idx32;
+  int32_t pad;
   FieldDesc f[kMaxFields];
 };
 
@@ -129,15 +133,6 @@ __device__ __forceinline__ int block_tile() {
 #else
   return static_cast<int>(blockIdx.x);
 #endif
-}
-
-__device__ __forceinline__ int find_field(const PoolParams& p, int tile) {
-  int lo = 0, hi = p.num_fields - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.f[mid].tile_begin <= tile) lo = mid; else hi = mid - 1;
-  }
-  return lo;
 }
 
 __device__ __forceinline__ int64_t load_index(const PoolParams& p, int64_t e) {
@@ -165,27 +160,29 @@ struct Shape {
 };
 
 // Accumulate the rows of elements [s0, s1) into this lane's columns; subgroup g of the
-// wavefront takes elements s0 + g, s0 + g + R, ... in order. Wave-uniform s0, s1.
+// wavefront takes elements s0 + g, s0 + g + R, ... in order. Wave-uniform s0, s1. `ids` is this
+// wavefront's private 64-entry LDS slice for row ids: its accesses are ordered by program order
+// within the wavefront, so no workgroup barrier is involved.
 template <typename TT, int LANES, int VPL>
 __device__ __forceinline__ void wave_slice_partial(const PoolParams& p, const char* table, int64_t max_row,
-                                                   int64_t row_bytes, int64_t s0, int64_t s1, float* pa) {
+                                                   int64_t row_bytes, int64_t s0, int64_t s1, float* pa,
+                                                   unsigned int* ids) {
   using S = Shape<TT, LANES, VPL>;
   const int lane = lane_id();
   const int g = lane / LANES, sl = lane % LANES;
   for (int64_t c = s0; c < s1; c += kWave) {
-    int64_t roff = 0;
-    if (c + lane < s1) roff = clamp_i64(load_index(p, c + lane), 0, max_row) * row_bytes;
+    ids[lane] = c + lane < s1 ? static_cast<unsigned int>(clamp_i64(load_index(p, c + lane), 0, max_row)) : 0u;
     const int n = static_cast<int>(s1 - c < kWave ? s1 - c : kWave);
     for (int k = 0; k < n; k += S::U * S::R) {
       uint4 v[S::U][VPL];
 #pragma unroll
       for (int u = 0; u < S::U; ++u) {
         const int e = k + u * S::R + g;  // < 64 because U * R <= 64
-        const int64_t ro = shfl_i64(roff, e);
+        const char* row = table + static_cast<uint64_t>(ids[e]) * static_cast<uint64_t>(row_bytes);
         const bool act = e < n;
 #pragma unroll
         for (int q = 0; q < VPL; ++q)
-          v[u][q] = act ? load_row16(table + ro + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
+          v[u][q] = act ? load_row16(row + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
       for (int u = 0; u < S::U; ++u) {
@@ -216,14 +213,44 @@ __device__ __forceinline__ void store_bag(const PoolParams& p, int64_t b, int ou
   for (int q = 0; q < VPL; ++q) store_out<S::VEC>(o + (q * LANES + sl) * S::VEC, a + q * S::VEC);
 }
 
-// Main kernel: one wavefront, one tile of R bags of one field.
+// U row loads of one step: elements k .. k+U-1 of this subgroup's current chunk, whose row ids
+// are in `ids` (the subgroup's slice of the wavefront's LDS row-id buffer; immediate offsets).
+template <typename TT, int LANES, int VPL>
+__device__ __forceinline__ void load_step(const char* table, int64_t row_bytes, const unsigned int* ids, int sl,
+                                          int k, int live, uint4 (&v)[Shape<TT, LANES, VPL>::U][VPL]) {
+  using S = Shape<TT, LANES, VPL>;
+#pragma unroll
+  for (int u = 0; u < S::U; ++u) {
+    const unsigned int r = ids[k + u];
+    const char* row = table + static_cast<uint64_t>(r) * static_cast<uint64_t>(row_bytes);
+    const bool act = k + u < live;
+#pragma unroll
+    for (int q = 0; q < VPL; ++q)
+      v[u][q] = act ? load_row16(row + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+template <typename TT, int LANES, int VPL>
+__device__ __forceinline__ void add_step(float* acc, const uint4 (&v)[Shape<TT, LANES, VPL>::U][VPL]) {
+  using S = Shape<TT, LANES, VPL>;
+#pragma unroll
+  for (int u = 0; u < S::U; ++u) {
+#pragma unroll
+    for (int q = 0; q < VPL; ++q) acc16(acc + q * S::VEC, v[u][q], TT{});
+  }
+}
+
+// One tile of R bags of one field, pooled by one wavefront:
+//   short (L <= sub_threshold): one subgroup per bag, rows in element order;
+//   medium (sub_threshold < L <= block_threshold): the whole wavefront, one bag at a time;
+//   long (L > block_threshold): left to the long kernel.
+// A chunk of LANES row ids per subgroup is loaded once (one lane per id, coalesced), clamped, and
+// broadcast through the wavefront's LDS slice; each step then issues U row loads per lane.
 template <typename TT, typename OT, int LANES, int VPL>
-__global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
+__device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, unsigned int* s_ids) {
   using S = Shape<TT, LANES, VPL>;
   constexpr int U = S::U;
-
-  const int tile = block_tile();
-  const int fi = find_field(p, tile);
+  const int fi = tile / p.tiles_per_field;
   const char* const table = p.f[fi].table;
   const int64_t max_row = p.f[fi].max_row;
   const int64_t row_bytes = p.f[fi].row_bytes;
@@ -234,52 +261,32 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
   const int g = lane / LANES;   // subgroup inside the wavefront
   const int sl = lane % LANES;  // lane inside the subgroup
 
-  if (p.bin_count && blockIdx.x == 0 && threadIdx.x == 0) {
-    // hand the finished list length to the long kernel and zero the counter for the next call
-    const unsigned int n = __hip_atomic_load(p.bin_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.bin_total, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.bin_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-  const int64_t b = static_cast<int64_t>(tile - p.f[fi].tile_begin) * S::R + g;
+  const int64_t b = static_cast<int64_t>(tile - fi * p.tiles_per_field) * S::R + g;
   const bool valid = b < p.batch;
   int64_t start = 0, end = 0;
   if (valid) bag_range(p, gidx, b, start, end);
   const int64_t L = end - start;
   const bool medium = valid && L > p.sub_threshold && L <= p.block_threshold;
-  const bool mine = valid && L <= p.sub_threshold;  // pooled by this subgroup
+  const bool mine = valid && L <= p.sub_threshold;  // pooled by this subgroup (empty bags too)
   const int64_t Ls = mine ? L : 0;
 
-  // ---- short bags: one subgroup per bag, rows accumulated in order -------------------------
   float acc[S::NACC];
 #pragma unroll
   for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
-
-  const int64_t maxL = wave_max_i64(Ls);
-  for (int64_t c = 0; c < maxL; c += LANES) {
-    int64_t roff = 0;
-    if (c + sl < Ls) roff = clamp_i64(load_index(p, start + c + sl), 0, max_row) * row_bytes;
-    const int n = static_cast<int>(maxL - c < LANES ? maxL - c : LANES);
-    for (int k = 0; k < n; k += U) {
+  for (int64_t c = 0; __ballot(c < Ls) != 0; c += LANES) {
+    __syncthreads();  // one wavefront per workgroup: orders this chunk's LDS writes after the last reads
+    s_ids[lane] = c + sl < Ls ? static_cast<unsigned int>(clamp_i64(load_index(p, start + c + sl), 0, max_row)) : 0u;
+    __syncthreads();
+    const int live = Ls - c < LANES ? static_cast<int>(Ls - c) : LANES;
+    for (int k = 0; k < LANES; k += U) {
+      if (__ballot(k < live) == 0) break;
       uint4 v[U][VPL];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t ro = shfl_i64(roff, g * LANES + k + u);
-        const bool act = c + k + u < Ls;
-#pragma unroll
-        for (int q = 0; q < VPL; ++q)
-          v[u][q] = act ? load_row16(table + ro + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int q = 0; q < VPL; ++q) acc16(acc + q * S::VEC, v[u][q], TT{});
-      }
+      load_step<TT, LANES, VPL>(table, row_bytes, s_ids + g * LANES, sl, k, live, v);
+      add_step<TT, LANES, VPL>(acc, v);
     }
   }
   if (mine) store_bag<TT, OT, LANES, VPL>(p, b, out_col, L, acc);
 
-  // ---- medium bags: the whole wavefront on one bag at a time -------------------------------
   uint64_t m = __ballot(medium && sl == 0);
   while (m) {
     const int src = __ffsll(static_cast<long long>(m)) - 1;  // lane 0 of the owning subgroup
@@ -288,9 +295,26 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
     float pa[S::NACC];
 #pragma unroll
     for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
-    wave_slice_partial<TT, LANES, VPL>(p, table, max_row, row_bytes, bs, be, pa);
+    wave_slice_partial<TT, LANES, VPL>(p, table, max_row, row_bytes, bs, be, pa, s_ids);
     if (g == 0) store_bag<TT, OT, LANES, VPL>(p, bb, out_col, be - bs, pa);
   }
+}
+
+__device__ __forceinline__ void bin_handoff(const PoolParams& p) {
+  if (p.bin_count && blockIdx.x == 0 && threadIdx.x == 0) {
+    // hand the finished list length to the long kernel and zero the counter for the next call
+    const unsigned int n = __hip_atomic_load(p.bin_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.bin_total, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.bin_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Main kernel: one wavefront per workgroup, one tile per workgroup.
+template <typename TT, typename OT, int LANES, int VPL>
+__global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
+  __shared__ unsigned int s_ids[kWave];
+  bin_handoff(p);
+  pool_tile<TT, OT, LANES, VPL>(p, block_tile(), s_ids);
 }
 
 // Length-binning pass: list the bags longer than block_threshold. grid (ceil(B/256), fields).
@@ -320,6 +344,7 @@ template <typename TT, typename OT, int LANES, int VPL, int LW>
 __global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams p, LongList l) {
   using S = Shape<TT, LANES, VPL>;
   __shared__ float s_red[LW * S::D];
+  __shared__ unsigned int s_ids[LW * kWave];
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) >> 6;
   const int g = lane / LANES, sl = lane % LANES;
@@ -336,7 +361,8 @@ __global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams 
     float pa[S::NACC];
 #pragma unroll
     for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
-    wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].max_row, p.f[fi].row_bytes, s0, s1, pa);
+    wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].max_row, p.f[fi].row_bytes, s0, s1, pa,
+                                       s_ids + wave * kWave);
     if (g == 0) {
 #pragma unroll
       for (int q = 0; q < VPL; ++q) {
@@ -370,14 +396,14 @@ template <typename TT, typename OT>
 __global__ void __launch_bounds__(kMainThreads) pool_generic_kernel(const PoolParams p) {
   constexpr int NC = 4;
   const int tile = block_tile();
-  const int fi = find_field(p, tile);
+  const int fi = tile / p.tiles_per_field;
   const char* const table = p.f[fi].table;
   const int64_t max_row = p.f[fi].max_row;
   const int64_t row_bytes = p.f[fi].row_bytes;
   const int dim = p.f[fi].dim;
   const int out_col = p.f[fi].out_col;
   const int lane = lane_id();
-  const int64_t b = static_cast<int64_t>(tile - p.f[fi].tile_begin);
+  const int64_t b = static_cast<int64_t>(tile - fi * p.tiles_per_field);
   if (b >= p.batch) return;
   int64_t start, end;
   bag_range(p, p.f[fi].gidx, b, start, end);
@@ -525,6 +551,8 @@ int validate_tables(const Job& j) {
     const cti_ebag_table& t = j.tables[f];
     if (!t.data) return set_error(CTI_EBAG_EINVAL, "table %d: data is NULL", f);
     if (t.rows < 1) return set_error(CTI_EBAG_EINVAL, "table %d: rows must be >= 1 (got %lld)", f, (long long)t.rows);
+    if (t.rows > INT32_MAX)
+      return set_error(CTI_EBAG_EUNSUPPORTED, "table %d: more than 2^31 - 1 rows (%lld)", f, (long long)t.rows);
     if (t.dim < 1) return set_error(CTI_EBAG_EINVAL, "table %d: dim must be >= 1 (got %d)", f, t.dim);
     if (t.row_stride < t.dim) return set_error(CTI_EBAG_EINVAL, "table %d: row_stride %lld < dim %d", f, (long long)t.row_stride, t.dim);
     if (t.out_col < 0 || static_cast<int64_t>(t.out_col) + t.dim > j.out_row_stride)
@@ -587,9 +615,9 @@ int run_job(const Job& j, hipStream_t stream) {
         d.dim = t.dim;
         d.out_col = t.out_col;
         d.gidx = f;
-        d.tile_begin = static_cast<int32_t>(tiles_per_field * static_cast<int64_t>(i));
       }
       p.num_tiles = static_cast<int32_t>(tiles_per_field * static_cast<int64_t>(nf));
+      p.tiles_per_field = static_cast<int32_t>(tiles_per_field);
       const hipError_t e = launch_typed(j.tdt, j.odt, v, p, bins ? &list : nullptr, stream);
       if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "pooling kernel launch failed: %s", hipGetErrorString(e));
     }
@@ -618,6 +646,7 @@ extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* va
   if (num_slots < 0) return set_error(CTI_EBAG_EINVAL, "num_slots must be >= 0 (got %d)", num_slots);
   if (emb_dim < 1) return set_error(CTI_EBAG_EINVAL, "emb_dim must be >= 1 (got %d)", emb_dim);
   if (max_idx < 0) return set_error(CTI_EBAG_EINVAL, "max_idx must be >= 0 (got %lld)", (long long)max_idx);
+  if (max_idx >= INT32_MAX) return set_error(CTI_EBAG_EUNSUPPORTED, "max_idx must be < 2^31 - 1 (got %lld)", (long long)max_idx);
   if (nnz < 0) return set_error(CTI_EBAG_EINVAL, "nnz must be >= 0 (got %lld)", (long long)nnz);
   if (!dtype_ok(dtype)) return set_error(CTI_EBAG_EINVAL, "unknown dtype code %d", dtype);
   if (batch_size == 0 || num_slots == 0) return CTI_EBAG_OK;
