@@ -99,6 +99,29 @@ def test_against_torch_library_routines(cfg, pooling):
     np.testing.assert_allclose(got, eb, rtol=0, atol=5e-5)
 
 
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+@pytest.mark.parametrize("kind", ["normal", "int"])
+def test_cpu_loops_match_the_c_oracle(pooling, kind):
+    """oracle/cpu_loops.py (the CPU baseline's loops) against pool_c: exact on integer rows,
+    within the fp32 reassociation bound otherwise; clamp cases and empty bags included."""
+    from oracle import cpu_loops
+
+    case = random_case(300, F=4, B=33, dims=(64, 128), V=(500,), tdt="f32", kind=kind, max_len=40,
+                       long_every=7, long_len=200)
+    got = orc.pool_c(case.values, case.offsets, case.tables, "f32", pooling, "f32")
+    vals = torch.from_numpy(case.values)
+    offs = torch.from_numpy(case.offsets)
+    tables = [torch.from_numpy(orc.decode(t, "f32").copy()) for t in case.tables]
+    _, bound = f64_reference(case, pooling)
+    for loop in (cpu_loops.baseline_loop, cpu_loops.embedding_bag_loop):
+        ref = loop(vals, offs, tables, pooling, case.B).numpy()
+        assert ref.shape == got.shape
+        if kind == "int" and pooling == "sum":
+            assert np.array_equal(ref, got), loop.__name__
+        else:
+            assert np.all(np.abs(ref - got) <= 2 * bound + 1e-30), loop.__name__
+
+
 def test_reference_layout_equals_global_layout():
     case = random_case(7, F=6, B=31, dims=(64,), V=(400,), tdt="bf16")
     ro, vo = case.reference_layout()
