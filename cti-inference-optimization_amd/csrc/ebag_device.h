@@ -22,14 +22,6 @@ struct f16_t {
 // bf16 -> fp32 is exact: the bf16 word is the high half of the fp32 word.
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// fp32 -> bf16, IEEE round-to-nearest-even on the 16 discarded bits. NaN stays NaN (quiet bit
-// forced) with its sign; +-Inf and values that round past the largest finite bf16 become +-Inf.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x0040u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
-
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return __half2float(__ushort_as_half(static_cast<unsigned short>(h)));
 }
@@ -100,6 +92,15 @@ __device__ __forceinline__ void store_out(float* dst, const float* a) {
     *reinterpret_cast<uint4*>(dst + i) = v;
   }
 }
+// Two fp32 values to a packed bf16 pair, IEEE round to nearest even (one v_cvt_pk_bf16_f32 on
+// gfx950): +-Inf and values that round past the largest finite bf16 become +-Inf, NaN stays NaN.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
 template <int N>
 __device__ __forceinline__ void store_out(bf16_t* dst, const float* a) {
   static_assert(N % 4 == 0, "16-bit stores are 8- or 16-byte vectors");
@@ -107,18 +108,18 @@ __device__ __forceinline__ void store_out(bf16_t* dst, const float* a) {
 #pragma unroll
     for (int i = 0; i < N; i += 8) {
       uint4 v;
-      v.x = f32_to_bf16_bits(a[i]) | (f32_to_bf16_bits(a[i + 1]) << 16);
-      v.y = f32_to_bf16_bits(a[i + 2]) | (f32_to_bf16_bits(a[i + 3]) << 16);
-      v.z = f32_to_bf16_bits(a[i + 4]) | (f32_to_bf16_bits(a[i + 5]) << 16);
-      v.w = f32_to_bf16_bits(a[i + 6]) | (f32_to_bf16_bits(a[i + 7]) << 16);
+      v.x = pack_bf16x2(a[i], a[i + 1]);
+      v.y = pack_bf16x2(a[i + 2], a[i + 3]);
+      v.z = pack_bf16x2(a[i + 4], a[i + 5]);
+      v.w = pack_bf16x2(a[i + 6], a[i + 7]);
       *reinterpret_cast<uint4*>(dst + i) = v;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < N; i += 4) {
       uint2 v;
-      v.x = f32_to_bf16_bits(a[i]) | (f32_to_bf16_bits(a[i + 1]) << 16);
-      v.y = f32_to_bf16_bits(a[i + 2]) | (f32_to_bf16_bits(a[i + 3]) << 16);
+      v.x = pack_bf16x2(a[i], a[i + 1]);
+      v.y = pack_bf16x2(a[i + 2], a[i + 3]);
       *reinterpret_cast<uint2*>(dst + i) = v;
     }
   }
@@ -149,10 +150,36 @@ __device__ __forceinline__ void store_out(f16_t* dst, const float* a) {
 
 __device__ __forceinline__ void store_one(float* dst, float a) { *dst = a; }
 __device__ __forceinline__ void store_one(bf16_t* dst, float a) {
-  *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(f32_to_bf16_bits(a));
+  *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(pack_bf16x2(a, 0.f));
 }
 __device__ __forceinline__ void store_one(f16_t* dst, float a) {
   *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(f32_to_f16_bits(a));
+}
+
+// a[i] / L for a bag of L >= 1 rows, each rounded once to fp32, given inv = 1/L rounded to fp64.
+// For quotients in the normal range RN32(RN64(a * inv)) = RN32(a / L): the fp64 product is
+// within 2^-52 (relative) of a / L, and a / L (a has a 24-bit significand, L <= 2^24) is at
+// least 2^-49 (relative) away from every fp32 rounding midpoint it is not equal to, while it
+// is never equal to one there (its odd part has at most 24 bits). Quotients below the normal
+// range, where a midpoint can be hit exactly, and zero sums are recomputed by IEEE division (a
+// branch that is rarely taken for real data).
+template <int N>
+__device__ __forceinline__ void div_by_count(float* a, double inv, float fl) {
+  // |a| < 2^-126 * L (exact: L <= 2^24) <=> the quotient is below the normal range (or zero)
+  const float tiny = 1.17549435e-38f * fl;
+  float q[N];
+  bool fix = false;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    q[i] = static_cast<float>(static_cast<double>(a[i]) * inv);
+    fix |= __builtin_fabsf(a[i]) < tiny;
+  }
+  if (__builtin_expect(fix, 0)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) q[i] = __builtin_fabsf(a[i]) < tiny ? a[i] / fl : q[i];
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) a[i] = q[i];
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -172,15 +199,6 @@ __device__ __forceinline__ int64_t shfl_i64(int64_t v, int src_lane) {
 __device__ __forceinline__ float shfl_xor_f32(float v, int mask) {
   return __int_as_float(shfl_i32(__float_as_int(v), lane_id() ^ mask));
 }
-__device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const int64_t o = shfl_i64(v, lane_id() ^ m);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
 __device__ __forceinline__ uint4 load16(const char* p) {
   return *reinterpret_cast<const uint4*>(p);
 }

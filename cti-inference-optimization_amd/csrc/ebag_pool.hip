@@ -5,21 +5,29 @@
 //   out[b, col_f + d] = pool_{i in bag(f, b)} table_f[clamp(values[i], 0, rows_f - 1), d]
 // with fp32 accumulation, empty bag -> 0, and one rounding to the output type.
 //
-// This is a memory-bound gather (no matrix cores). Work decomposition:
+// This is a gather (no matrix cores); on MI355X it is bound by vector-ALU issue and memory latency
+// more than by HBM bandwidth, so the design keeps VALU work per pooled row small. Decomposition:
 //   * A row of D elements is read as 16-byte vectors by LANES = row_bytes/16 lanes, so a 64-lane
 //     wavefront holds R = 64/LANES lane groups ("subgroups"). For D = 128 bf16: 16 lanes x 16 B
 //     per row, 4 subgroups per wavefront.
-//   * Main kernel: one wavefront per workgroup, one tile of R consecutive bags of one field.
-//       - short bag (L <= sub_threshold): pooled by one subgroup; each lane adds its columns of
-//         the bag's rows in element order, so the result equals a sequential fp32 sum bit for bit;
+//   * Main kernel: one wavefront per workgroup, one tile of ROUNDS * R consecutive bags of one
+//     field. The tile's short bags are ranked by length and pooled R at a time, one bag per
+//     subgroup, so the bags pooled side by side need about the same number of steps:
+//       - short bag (L <= sub_threshold): each lane adds its columns of the bag's rows in element
+//         order, so the result equals a sequential fp32 sum bit for bit;
 //       - medium bag (sub_threshold < L <= block_threshold): split over the wavefront's subgroups
 //         (interleaved rows), partials combined with an xor butterfly in a fixed order;
 //       - long bag (L > block_threshold, only with the length-binning pass): left to the long kernel.
 //     Single-wavefront workgroups need no workgroup barrier, so a wavefront retires as soon as its
-//     own bags are done (measured: 4-wavefront workgroups are ~10% slower on D=128 bf16).
-//     ROWS_IN_FLIGHT row loads per lane are issued before any is consumed. Row ids are clamped,
-//     narrowed to 32 bits (tables have < 2^31 rows) and broadcast to the lanes that read the row
-//     through LDS (one immediate-offset read per row instead of a lane shuffle per row).
+//     own bags are done (measured: multi-wavefront workgroups are slower, also when they share a
+//     length ranking). Row ids are clamped, narrowed to 32 bits (tables have < 2^31 rows) and
+//     broadcast through LDS; a step reads ROWS_IN_FLIGHT ids, then issues that many row loads
+//     before consuming any. Tables under 4 GiB with power-of-two row sizes are read with buffer
+//     loads: a row's offset is one shift-add, and rows past a bag's end use an out-of-range offset
+//     that returns zeros without a memory request (no per-row branch).
+//   * Mean: one fp64 reciprocal per bag, RN32(RN64(sum * 1/L)) per element, which equals the IEEE
+//     fp32 division except for quotients below the normal range (those take the division).
+//     Conversions to bf16 use the hardware round-to-nearest-even pack.
 //   * Length-binning pass (optional): one thread per bag; bags longer than block_threshold are
 //     appended to a list in the caller's workspace (one atomic per wavefront).
 //   * Long kernel: 8 wavefronts (4 for 2 KB rows) per workgroup, looping over the list; each bag
@@ -55,6 +63,9 @@ namespace {
 #ifndef CTI_EBAG_NT_ROWS
 #define CTI_EBAG_NT_ROWS 0  // non-temporal hint on table-row loads
 #endif
+#ifndef CTI_EBAG_ROUNDS
+#define CTI_EBAG_ROUNDS 2  // rounds of R length-ranked bags per tile of the main kernel
+#endif
 
 constexpr int kMainThreads = kWave;  // main kernel: one wavefront per workgroup
 constexpr int kBinThreads = 256;
@@ -87,7 +98,7 @@ struct FieldDesc {
   int32_t dim;         // columns pooled
   int32_t out_col;     // first output column
   int32_t gidx;        // field index used for offsets / val_base
-  int32_t pad;
+  uint32_t span_bytes; // bytes from row 0 to the end of the last row, when below 4 GiB (else 0)
 };
 
 struct PoolParams {
@@ -108,7 +119,7 @@ struct PoolParams {
   int32_t tiles_per_field;  // every field of a launch has the same number of tiles
   int32_t pooling;          // CTI_EBAG_SUM / CTI_EBAG_MEAN
   int32_t idx32;
-  int32_t pad;
+  int32_t buffer_ok;        // every field's span_bytes is set: rows are read with buffer loads
   FieldDesc f[kMaxFields];
 };
 
@@ -133,6 +144,19 @@ __device__ __forceinline__ int block_tile() {
 #else
   return static_cast<int>(blockIdx.x);
 #endif
+}
+
+// Buffer resource over one table: 32-bit byte offsets, offsets at or past the span read as zeros.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr unsigned int kOutOfRange = 0xfffffff0u;  // above every span accepted by the host
+__device__ __forceinline__ Rsrc make_rsrc(const char* base, uint32_t span) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), static_cast<short>(0), static_cast<int>(span),
+                                           0x00020000);  // raw buffer, 32-bit data format
+}
+__device__ __forceinline__ uint4 buffer_load16(Rsrc r, unsigned int off) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ int64_t load_index(const PoolParams& p, int64_t e) {
@@ -203,14 +227,13 @@ template <typename TT, typename OT, int LANES, int VPL>
 __device__ __forceinline__ void store_bag(const PoolParams& p, int64_t b, int out_col, int64_t L, float* a) {
   using S = Shape<TT, LANES, VPL>;
   const int sl = lane_id() % LANES;
-  if (p.pooling == CTI_EBAG_MEAN && L > 0) {
-    const float fl = static_cast<float>(L);
+  float r[S::NACC];
 #pragma unroll
-    for (int i = 0; i < S::NACC; ++i) a[i] = a[i] / fl;
-  }
+  for (int i = 0; i < S::NACC; ++i) r[i] = a[i];
+  if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<S::NACC>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
   OT* o = reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col;
 #pragma unroll
-  for (int q = 0; q < VPL; ++q) store_out<S::VEC>(o + (q * LANES + sl) * S::VEC, a + q * S::VEC);
+  for (int q = 0; q < VPL; ++q) store_out<S::VEC>(o + (q * LANES + sl) * S::VEC, r + q * S::VEC);
 }
 
 // U row loads of one step: elements k .. k+U-1 of this subgroup's current chunk, whose row ids
@@ -240,63 +263,125 @@ __device__ __forceinline__ void add_step(float* acc, const uint4 (&v)[Shape<TT, 
   }
 }
 
-// One tile of R bags of one field, pooled by one wavefront:
-//   short (L <= sub_threshold): one subgroup per bag, rows in element order;
+// Tile of the main kernel: ROUNDS rounds of R bags (R = lane groups per wavefront).
+template <typename TT, int LANES, int VPL>
+struct TileShape {
+  static constexpr int R = kWave / LANES;
+  static constexpr int ROUNDS = CTI_EBAG_ROUNDS * R <= kWave ? CTI_EBAG_ROUNDS : kWave / R;
+  static constexpr int NB = R * ROUNDS;  // bags per tile
+};
+
+template <int NB>
+struct TileLds {
+  unsigned int ids[kWave];  // row ids of the current chunk, LANES per subgroup
+  int order[NB];            // tile bags by rank: short bags, longest first
+  int len[NB];
+  int64_t start[NB];
+};
+
+template <typename TT, int LANES, int VPL>
+using TileLdsOf = TileLds<TileShape<TT, LANES, VPL>::NB>;
+
+// One tile of NB consecutive bags of one field, pooled by one wavefront:
+//   short (L <= sub_threshold): one subgroup per bag, rows in element order. The short bags are
+//     ranked by length and taken R at a time, longest first, so the R bags pooled side by side
+//     need about the same number of steps;
 //   medium (sub_threshold < L <= block_threshold): the whole wavefront, one bag at a time;
 //   long (L > block_threshold): left to the long kernel.
 // A chunk of LANES row ids per subgroup is loaded once (one lane per id, coalesced), clamped, and
 // broadcast through the wavefront's LDS slice; each step then issues U row loads per lane.
-template <typename TT, typename OT, int LANES, int VPL>
-__device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, unsigned int* s_ids) {
+template <typename TT, typename OT, int LANES, int VPL, bool BUF>
+__device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLdsOf<TT, LANES, VPL>& s) {
   using S = Shape<TT, LANES, VPL>;
   constexpr int U = S::U;
+  constexpr int R = S::R;
+  constexpr int NB = TileShape<TT, LANES, VPL>::NB;
   const int fi = tile / p.tiles_per_field;
   const char* const table = p.f[fi].table;
   const int64_t max_row = p.f[fi].max_row;
   const int64_t row_bytes = p.f[fi].row_bytes;
   const int gidx = p.f[fi].gidx;
   const int out_col = p.f[fi].out_col;
+  const Rsrc rsrc = make_rsrc(table, BUF ? p.f[fi].span_bytes : 0u);
+  const unsigned int shift = static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(row_bytes)));
 
   const int lane = lane_id();
   const int g = lane / LANES;   // subgroup inside the wavefront
   const int sl = lane % LANES;  // lane inside the subgroup
+  const int64_t b0 = static_cast<int64_t>(tile - fi * p.tiles_per_field) * NB;
 
-  const int64_t b = static_cast<int64_t>(tile - fi * p.tiles_per_field) * S::R + g;
-  const bool valid = b < p.batch;
+  // Lane i describes bag b0 + i.
+  const bool valid = lane < NB && b0 + lane < p.batch;
   int64_t start = 0, end = 0;
-  if (valid) bag_range(p, gidx, b, start, end);
+  if (valid) bag_range(p, gidx, b0 + lane, start, end);
   const int64_t L = end - start;
+  const bool shortb = valid && L <= p.sub_threshold;  // empty bags too; sub_threshold < 2^24 (host)
   const bool medium = valid && L > p.sub_threshold && L <= p.block_threshold;
-  const bool mine = valid && L <= p.sub_threshold;  // pooled by this subgroup (empty bags too)
-  const int64_t Ls = mine ? L : 0;
-
-  float acc[S::NACC];
+  const int n_short = __popcll(__ballot(shortb));
+  // rank among the short bags: longer first, ties by position
+  const int key = shortb ? static_cast<int>(L) : -1;
+  int rank = 0;
 #pragma unroll
-  for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
-  for (int64_t c = 0; __ballot(c < Ls) != 0; c += LANES) {
-    __syncthreads();  // one wavefront per workgroup: orders this chunk's LDS writes after the last reads
-    s_ids[lane] = c + sl < Ls ? static_cast<unsigned int>(clamp_i64(load_index(p, start + c + sl), 0, max_row)) : 0u;
-    __syncthreads();
-    const int live = Ls - c < LANES ? static_cast<int>(Ls - c) : LANES;
-    for (int k = 0; k < LANES; k += U) {
-      if (__ballot(k < live) == 0) break;
-      uint4 v[U][VPL];
-      load_step<TT, LANES, VPL>(table, row_bytes, s_ids + g * LANES, sl, k, live, v);
-      add_step<TT, LANES, VPL>(acc, v);
-    }
+  for (int j = 0; j < NB; ++j) {
+    const int kj = __builtin_amdgcn_readlane(key, j);
+    rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
   }
-  if (mine) store_bag<TT, OT, LANES, VPL>(p, b, out_col, L, acc);
+  if (shortb) {
+    s.order[rank] = lane;
+    s.len[lane] = static_cast<int>(L);
+    s.start[lane] = start;
+  }
+  __syncthreads();  // one wavefront per workgroup: orders the bag table before other lanes read it
 
-  uint64_t m = __ballot(medium && sl == 0);
-  while (m) {
-    const int src = __ffsll(static_cast<long long>(m)) - 1;  // lane 0 of the owning subgroup
+  for (int r0 = 0; r0 < n_short; r0 += R) {
+    const int slot = r0 + g;
+    const bool has = slot < n_short;
+    const int bi = has ? s.order[slot] : 0;
+    const int Lb = has ? s.len[bi] : 0;
+    const int64_t bs = has ? s.start[bi] : 0;
+    float acc[S::NACC];
+#pragma unroll
+    for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
+    for (int c = 0; __ballot(c < Lb) != 0; c += LANES) {
+      __syncthreads();  // orders this chunk's LDS writes after the last reads
+      s.ids[lane] = c + sl < Lb ? static_cast<unsigned int>(clamp_i64(load_index(p, bs + c + sl), 0, max_row)) : 0u;
+      __syncthreads();
+      const int live = Lb - c < LANES ? Lb - c : LANES;
+      for (int k = 0; k < LANES; k += U) {
+        if (__ballot(k < live) == 0) break;
+        uint4 v[U][VPL];
+        if constexpr (BUF) {
+          // all U ids first, then branch-free loads (out-of-range offsets read as zeros)
+          unsigned int r[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) r[u] = s.ids[g * LANES + k + u];
+          const unsigned int lane_off = static_cast<unsigned int>(sl * 16);
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const unsigned int o = (r[u] << shift) + lane_off;
+#pragma unroll
+            for (int q = 0; q < VPL; ++q) v[u][q] = buffer_load16(rsrc, k + u < live ? o + q * LANES * 16 : kOutOfRange);
+          }
+          __builtin_amdgcn_sched_barrier(0);  // issue every load of the step before consuming any
+        } else {
+          load_step<TT, LANES, VPL>(table, row_bytes, s.ids + g * LANES, sl, k, live, v);
+        }
+        add_step<TT, LANES, VPL>(acc, v);
+      }
+    }
+    if (has) store_bag<TT, OT, LANES, VPL>(p, b0 + bi, out_col, Lb, acc);
+  }
+
+  for (uint64_t m = __ballot(medium); m;) {
+    const int src = __ffsll(static_cast<long long>(m)) - 1;  // the bag's lane
     m &= m - 1;
-    const int64_t bs = shfl_i64(start, src), be = shfl_i64(end, src), bb = shfl_i64(b, src);
+    const int64_t bs = shfl_i64(start, src), be = shfl_i64(end, src);
     float pa[S::NACC];
 #pragma unroll
     for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
-    wave_slice_partial<TT, LANES, VPL>(p, table, max_row, row_bytes, bs, be, pa, s_ids);
-    if (g == 0) store_bag<TT, OT, LANES, VPL>(p, bb, out_col, be - bs, pa);
+    __syncthreads();
+    wave_slice_partial<TT, LANES, VPL>(p, table, max_row, row_bytes, bs, be, pa, s.ids);
+    if (g == 0) store_bag<TT, OT, LANES, VPL>(p, b0 + src, out_col, be - bs, pa);
   }
 }
 
@@ -310,11 +395,11 @@ __device__ __forceinline__ void bin_handoff(const PoolParams& p) {
 }
 
 // Main kernel: one wavefront per workgroup, one tile per workgroup.
-template <typename TT, typename OT, int LANES, int VPL>
+template <typename TT, typename OT, int LANES, int VPL, bool BUF>
 __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
-  __shared__ unsigned int s_ids[kWave];
+  __shared__ TileLdsOf<TT, LANES, VPL> s;
   bin_handoff(p);
-  pool_tile<TT, OT, LANES, VPL>(p, block_tile(), s_ids);
+  pool_tile<TT, OT, LANES, VPL, BUF>(p, block_tile(), s);
 }
 
 // Length-binning pass: list the bags longer than block_threshold. grid (ceil(B/256), fields).
@@ -442,7 +527,11 @@ __global__ void __launch_bounds__(kMainThreads) pool_generic_kernel(const PoolPa
 // Host side
 // ---------------------------------------------------------------------------------------------
 int lanes_of(int variant) { return variant <= 6 ? (1 << variant) : 64; }
-int bags_per_tile(int variant) { return variant == kVarGeneric ? 1 : kWave / lanes_of(variant); }
+int bags_per_tile(int variant) {
+  if (variant == kVarGeneric) return 1;
+  const int r = kWave / lanes_of(variant);
+  return CTI_EBAG_ROUNDS * r <= kWave ? CTI_EBAG_ROUNDS * r : kWave;  // as TileShape::NB
+}
 
 #ifndef CTI_EBAG_SUB_THRESHOLD
 #define CTI_EBAG_SUB_THRESHOLD 48  // default: longer bags are split over the wavefront's subgroups
@@ -455,6 +544,8 @@ int64_t default_sub_threshold(int variant) {
 
 // With binning, bags longer than this go to the long kernel.
 constexpr int64_t kDefaultBlockThreshold = 512;
+// Longest bag pooled by one subgroup (longer ones are split over the wavefront).
+constexpr int64_t kMaxShortBag = int64_t{1} << 24;
 
 int pick_variant(const cti_ebag_table& t, int tb, int ob, const void* out, int64_t out_row_stride) {
   const int64_t row_bytes = static_cast<int64_t>(t.dim) * tb;
@@ -480,7 +571,11 @@ void launch_shape(const PoolParams& p, const LongList* l, hipStream_t s) {
     const dim3 bgrid(static_cast<unsigned>((p.batch + kBinThreads - 1) / kBinThreads), static_cast<unsigned>(p.num_fields));
     hipLaunchKernelGGL(bin_kernel, bgrid, dim3(kBinThreads), 0, s, p, *l);
   }
-  hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL>), dim3(static_cast<unsigned>(p.num_tiles)), dim3(kMainThreads), 0, s, p);
+const dim3 grid(static_cast<unsigned>(p.num_tiles)), block(kMainThreads);
+  if (p.buffer_ok)
+    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, false>), grid, block, 0, s, p);
   if (l) {
     constexpr int LW = VPL >= 4 ? 4 : 8;  // keeps the LDS partials at <= 32 KB
     // at most min(bags, nnz / (block_threshold + 1)) bags can be listed
@@ -597,6 +692,10 @@ int run_job(const Job& j, hipStream_t stream) {
       else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;
       const bool bins = j.use_bins && v != kVarGeneric;
       p.block_threshold = !bins ? kNoLimit : (j.block_threshold > 0 ? j.block_threshold : kDefaultBlockThreshold);
+      // a bag is pooled by exactly one kernel: never call a listed (long) bag short
+      if (v != kVarGeneric && p.sub_threshold > p.block_threshold) p.sub_threshold = p.block_threshold;
+      // short-bag lengths are kept in 32 bits on the device
+      if (v != kVarGeneric && p.sub_threshold > kMaxShortBag) p.sub_threshold = kMaxShortBag;
       p.bin_count = bins ? list.count : nullptr;
       p.bin_total = bins ? list.total : nullptr;
       const int bpt = bags_per_tile(v);
@@ -605,6 +704,7 @@ int run_job(const Job& j, hipStream_t stream) {
       if (tiles_per_field * static_cast<int64_t>(nf) > INT32_MAX)
         return set_error(CTI_EBAG_EUNSUPPORTED, "batch of %lld samples needs more than 2^31 tiles", (long long)j.batch);
       p.num_fields = static_cast<int32_t>(nf);
+      bool all_buf = true;
       for (size_t i = 0; i < nf; ++i) {
         const int f = fields[c0 + i];
         const cti_ebag_table& t = j.tables[f];
@@ -615,7 +715,12 @@ int run_job(const Job& j, hipStream_t stream) {
         d.dim = t.dim;
         d.out_col = t.out_col;
         d.gidx = f;
+        const int64_t span = (t.rows - 1) * d.row_bytes + static_cast<int64_t>(t.dim) * tb;
+        const bool pow2 = (d.row_bytes & (d.row_bytes - 1)) == 0;
+        d.span_bytes = pow2 && span < static_cast<int64_t>(kOutOfRange) ? static_cast<uint32_t>(span) : 0u;
+        all_buf = all_buf && d.span_bytes != 0;
       }
+      p.buffer_ok = all_buf ? 1 : 0;
       p.num_tiles = static_cast<int32_t>(tiles_per_field * static_cast<int64_t>(nf));
       p.tiles_per_field = static_cast<int32_t>(tiles_per_field);
       const hipError_t e = launch_typed(j.tdt, j.odt, v, p, bins ? &list : nullptr, stream);

@@ -237,6 +237,67 @@ def _reference_batch(seed, S=28, B=64, V=5000, D=128, dt="bf16", max_len=12):
     return case, ro, vo, case.tables[0]
 
 
+def _special_rows(D):
+    """Rows that exercise the fp32 sum and the output rounding at their edges."""
+    f32max = np.finfo(np.float32).max
+    tiny = np.float32(1e-40)  # fp32 subnormal
+    vals = [np.inf, -np.inf, np.nan, f32max, -f32max, 3.3961e38, tiny, -tiny, -0.0, 0.0,
+            1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 1.0 + 2.0 ** -11, 65504.0, 65520.0, 6e-8, 1e-45, 1.0]
+    rows = [np.full(D, v, np.float32) for v in vals]
+    rows.append(np.linspace(-3, 3, D).astype(np.float32))
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("tdt", ["f32", "bf16"])
+@pytest.mark.parametrize("odt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_special_values_match_oracle(pkg, dev, tdt, odt, pooling):
+    # bags of every pair, triple and single of the special rows (Inf, NaN, overflow, subnormals,
+    # rounding ties of bf16 / fp16, signed zeros); finite and infinite results bit for bit, NaN
+    # where the oracle has NaN
+    D = 128
+    table32 = _special_rows(D)
+    table = orc.encode(table32, tdt)
+    n = len(table32)
+    bags = [[i] for i in range(n)] + [[i, j] for i in range(n) for j in range(n)] + \
+           [[i, j, k] for i in range(0, n, 3) for j in range(1, n, 4) for k in range(2, n, 5)]
+    rng = np.random.default_rng(5)
+    rng.shuffle(bags)
+    B = len(bags)
+    lens = np.array([len(x) for x in bags])
+    values = np.concatenate([np.array(x, np.int64) for x in bags])
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    got = gpu_pool(pkg, dev, values, offsets, [table], tdt, pooling, odt, long_threshold=NO_SPLIT)
+    ref = orc.pool_c(values, offsets, [table], tdt, pooling, odt)
+    g, r = orc.decode(got, odt), orc.decode(ref, odt)
+    assert np.array_equal(np.isnan(g), np.isnan(r))
+    fin = ~np.isnan(r)
+    assert np.array_equal(got[fin], ref[fin])
+
+
+@pytest.mark.parametrize("long_threshold", [NO_SPLIT, 0])
+def test_mean_of_subnormal_midpoints(pkg, dev, long_threshold):
+    # bags whose fp32 mean is exactly halfway between two subnormals: (L - 1) rows of 2^-149 and
+    # one row of (m - L + 1) * 2^-149 sum to m * 2^-149, and m / L = (2k+1) / 2 (ties to even)
+    D = 64
+    cases = [(98, 147), (150, 2175), (154, 2233), (182, 1183), (186, 1209), (2, 3), (6, 9)]
+    rows = [np.full(D, 2.0 ** -149, np.float32)]
+    values, lens = [], []
+    for L, m in cases:
+        rows.append(np.full(D, (m - L + 1) * 2.0 ** -149, np.float32))
+        values += [0] * (L - 1) + [len(rows) - 1]
+        lens.append(L)
+    table = np.stack(rows)
+    values = np.array(values, np.int64)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    for odt in ("f32", "bf16", "f16"):
+        # sums of integer multiples of 2^-149 are exact in any order, so split bags
+        # (long_threshold 0) must match bit for bit as well
+        got = gpu_pool(pkg, dev, values, offsets, [table], "f32", "mean", odt, long_threshold=long_threshold)
+        ref = orc.pool_c(values, offsets, [table], "f32", "mean", odt)
+        assert np.array_equal(got, ref), odt
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f32", "f16"])
 def test_fused_all_slots_matches_oracle(pkg, dev, dt):
     case, ro, vo, w = _reference_batch(31, dt=dt)
