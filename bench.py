@@ -6,6 +6,10 @@ B = 4096 samples, geometric(mean 8) bag lengths, Zipf(1.1) ids, mean pooling, bf
 are resident in HBM before timing; step k uses index set k mod n_sets, so consecutive steps do
 not find each other's rows in L2 / MALL.
 
+`--stage layernorm` times the encoder's input LayerNorm instead (online_best/infer.py:1061-1076):
+the workload's batches are pooled once, and each step normalises one pooled block
+[B, sum(D)] (rows/s; roofline bytes = the block read and written plus gamma and beta).
+
 Printed (one JSON line): pooled bags/s over the timed steps, plus
   roofline     algorithmic bytes per launch / mean launch duration (one pair of HIP events
                around the K timed launches, on the stream the kernels run on), against 8 TB/s;
@@ -92,6 +96,50 @@ def cpu_baseline(wl, tables_dev, seconds):
                       f"F.embedding_bag per field (oracle/cpu_loops.py), {wl.table_dtype} tables in host memory"}
 
 
+def bench_layernorm(args, pkg, plan, inputs, wl0, dev):
+    """Time the input LayerNorm over pooled blocks of the workload (one block per step, rotated)."""
+    import torch
+
+    blocks = [plan(v, o) for v, o in inputs[:4]]
+    width = blocks[0].shape[1]
+    gen = torch.Generator(device=dev).manual_seed(0)
+    gamma = (1 + 0.1 * torch.randn(width, device=dev, generator=gen)).to(wl0.out_dtype)
+    beta = (0.1 * torch.randn(width, device=dev, generator=gen)).to(wl0.out_dtype)
+    out = torch.empty_like(blocks[0])
+    for i in range(args.warmup):
+        pkg.layer_norm(blocks[i % 4], gamma, beta, 1e-5, out=out)
+    K = args.steps
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    log(f"timing {K} LayerNorm steps over [{blocks[0].shape[0]}, {width}] {wl0.out_dtype}")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for i in range(K):
+        pkg.layer_norm(blocks[i % 4], gamma, beta, 1e-5, out=out)
+    ev1.record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    launch_s = ev0.elapsed_time(ev1) / 1e3 / K
+    nbytes = 2 * blocks[0].numel() * blocks[0].element_size() + 2 * width * gamma.element_size()
+    achieved = nbytes / launch_s / 1e9
+    log(f"{launch_s * 1e6:.2f} us/step on the GPU, {achieved:.0f} GB/s")
+    rec = {
+        "metric": "input LayerNorm rows/sec over the pooled block", "value": blocks[0].shape[0] / (elapsed / K),
+        "unit": "rows/s", "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": elapsed / K * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[wl0.out_dtype],
+        "data": "synthetic: pooled blocks of 4 seeded index sets rotated",
+        "config": {"workload": f"layernorm over the pooled {args.workload} block", "rows": blocks[0].shape[0],
+                   "cols": width},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "norm_rows_kernel",
+                     "bytes_per_launch": nbytes, "launch_us_mean": launch_s * 1e6},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +152,8 @@ def main():
     ap.add_argument("--long-threshold", type=int, default=0)
     ap.add_argument("--bins", action="store_true", help="run the device length-binning pass")
     ap.add_argument("--block-threshold", type=int, default=0)
+    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm"],
+                    help="time the pooling step (default) or the input LayerNorm over pooled blocks")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times (scales rocprofv3 FETCH/WRITE_SIZE) and exit")
     args = ap.parse_args()
@@ -144,6 +194,8 @@ def main():
     plan = pkg.PooledEmbedding(tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype, long_threshold=args.long_threshold,
                                use_bins=args.bins, block_threshold=args.block_threshold, max_batch=wl0.batch)
     out = torch.empty((wl0.batch, sum(wl0.dims)), dtype=wl0.out_dtype, device=dev)
+    if args.stage == "layernorm":
+        return bench_layernorm(args, pkg, plan, inputs, wl0, dev)
     bytes_alg = [wl.bytes_algorithmic() for wl in wls]
     bytes_comp = [wl.bytes_compulsory() for wl in wls]
     torch.cuda.synchronize()

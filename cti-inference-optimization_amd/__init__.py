@@ -5,7 +5,8 @@ Public surface:
   fused_embedding            the RepEncoder.forward fused step on a flat-layout batch dict
   embedding_bag_pooled       per-field tables, global offsets, sum/mean, chosen output dtype
   PooledEmbedding            the same with the table descriptors prepared once (serving loops)
-  RepEncoder                 the reference module with the fused step on this path
+  layer_norm                 the encoder's input LayerNorm over the pooled rows
+  RepEncoder                 the reference module with the fused step and LayerNorm on this path
   collate_flat_layout, prebuild_flat_layout   host builders of the flat layout
   pack_slots, merge_batches                   GPU builders of the flat layout
 """
@@ -13,7 +14,7 @@ from . import workloads
 from ._capi import EbagError, lib as load_library
 from .encoder import RepEncoder
 from .layout import collate_flat_layout, merge_batches, pack_slots, prebuild_flat_layout
-from .ops import PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_embedding
+from .ops import PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_embedding, layer_norm
 
 __all__ = [
     "EbagError",
@@ -27,5 +28,6 @@ __all__ = [
     "PooledEmbedding",
     "fused_all_slots_embedding",
     "fused_embedding",
+    "layer_norm",
     "workloads",
 ]

@@ -88,6 +88,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_PP, _PP, _PP, _PI64, _PI64, _I32, _I32, _P, _P, _P, _P, _P],
     ),
+    "cti_ebag_layernorm": (
+        ctypes.c_int,
+        [_P, _P, _I64, _I64, _I32, _P, _P, _I32, ctypes.c_float, _P, _P, _P],
+    ),
 }
 
 _lib = None

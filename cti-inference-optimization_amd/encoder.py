@@ -1,13 +1,12 @@
-"""RepEncoder with the fused embedding step on the HIP path.
+"""RepEncoder with the fused embedding step and the input LayerNorm on the HIP path.
 
 Mirrors the reference module online_best/infer.py:945-1100 (constructor signature, parameter
 names, forward(batch) contract): the 28 slots are pooled by ``fused_all_slots_embedding`` into
-``[B, slot_num*emb_dim]`` in the table's dtype, then LayerNorm(slot_num*emb_dim) and
-Linear(slot_num*emb_dim -> d_model) follow, as at online_best/infer.py:1061-1085.
-
-The LayerNorm and Linear here are torch's modules: they are downstream of the pooled output,
-whose layout (contiguous rows of slot_num*emb_dim, slot-major columns) is what this module
-guarantees them (online_best/infer.py:836-843).
+``[B, slot_num*emb_dim]`` in the table's dtype, the rows are normalised by ``layer_norm`` with
+the ``input_norm`` parameters (the reference's Triton LayerNorm, online_best/infer.py:1061-1076),
+and ``linear`` (torch's Linear, a plain library GEMM) maps them to d_model
+(online_best/infer.py:1084). Like the reference's Triton kernels, the pooling and the
+LayerNorm are forward-only (inference).
 """
 from __future__ import annotations
 
@@ -15,7 +14,7 @@ import torch
 from torch import nn
 
 from .layout import pack_slots
-from .ops import fused_all_slots_embedding
+from .ops import fused_all_slots_embedding, layer_norm
 
 
 class RepEncoder(nn.Module):
@@ -55,7 +54,12 @@ class RepEncoder(nn.Module):
             return fused_all_slots_embedding(flat_values, val_offsets, flat_row_offsets, weight.detach(), out,
                                              batch_size, self.emb_dim, self.emb.num_embeddings - 1)
 
-    def forward(self, batch: dict) -> torch.Tensor:
+    def normalized(self, batch: dict) -> torch.Tensor:
+        """Pooled rows after the input LayerNorm: ``[B, slot_num*emb_dim]`` in the table dtype."""
         fused_embs = self.pooled(batch)
-        norm_emb = self.input_norm(fused_embs)
-        return self.linear(norm_emb)
+        norm = self.input_norm
+        with torch.no_grad():
+            return layer_norm(fused_embs, norm.weight.detach(), norm.bias.detach(), norm.eps, out=fused_embs)
+
+    def forward(self, batch: dict) -> torch.Tensor:
+        return self.linear(self.normalized(batch))

@@ -281,3 +281,53 @@ class PooledEmbedding:
                              self.width, self._ws.data_ptr() if self._ws is not None else None, self._ws_bytes,
                              self._opts, stream))
         return out
+
+
+def layer_norm(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor,
+    eps: float = 1e-5,
+    out: Optional[torch.Tensor] = None,
+    mean: Optional[torch.Tensor] = None,
+    rstd: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Row LayerNorm of a 2-D GPU tensor ``x[rows, cols]`` (the encoder's input norm).
+
+    Mirrors ``layernorm_forward_kernel[(rows,)](x, y, gamma, beta, mean, rstd, eps, Row_Size)``
+    (online_best/infer.py:829-858, launched at online_best/infer.py:1063-1075): fp32 mean and
+    variance over each row, ``y = (x - mean) * rstd * weight + bias`` rounded once to x's dtype.
+    ``out`` (default: a new tensor like x, may be x itself), ``mean`` and ``rstd`` (optional,
+    fp32 ``[rows]``) are written on torch's current stream. Returns ``out``.
+    """
+    _require_device_tensor("x", x)
+    dev = x.device
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [rows, cols], got shape {tuple(x.shape)}")
+    _require_contiguous("x", x)
+    rows, cols = x.shape
+    for name, t in (("weight", weight), ("bias", bias)):
+        _require_device_tensor(name, t, dev)
+        _require_contiguous(name, t)
+        if t.numel() != cols:
+            raise ValueError(f"{name} has {t.numel()} elements, expected {cols}")
+    if weight.dtype != bias.dtype:
+        raise TypeError(f"weight and bias dtypes differ ({weight.dtype} vs {bias.dtype})")
+    if out is None:
+        out = torch.empty_like(x)
+    _require_device_tensor("out", out, dev)
+    _require_contiguous("out", out)
+    if out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError(f"out must be {tuple(x.shape)} {x.dtype}, got {tuple(out.shape)} {out.dtype}")
+    for name, t in (("mean", mean), ("rstd", rstd)):
+        if t is not None:
+            _require_device_tensor(name, t, dev)
+            if t.dtype != torch.float32 or t.numel() != rows or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous float32 tensor of {rows} elements")
+    lib = _capi.lib()
+    with torch.cuda.device(dev):
+        _capi.check(lib.cti_ebag_layernorm(
+            x.data_ptr(), out.data_ptr(), rows, cols, _capi.dtype_code(x.dtype), weight.data_ptr(), bias.data_ptr(),
+            _capi.dtype_code(weight.dtype), float(eps), mean.data_ptr() if mean is not None else None,
+            rstd.data_ptr() if rstd is not None else None, _capi.current_stream_handle(dev)))
+    return out

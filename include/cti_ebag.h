@@ -177,6 +177,21 @@ int cti_ebag_merge_batches(const int64_t* const* sub_values,
                            int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
                            int64_t* global_offsets, void* stream);
 
+/*
+ * Row LayerNorm over the pooled block, a drop-in for the launch
+ *   layernorm_forward_kernel[(rows,)](x, y, gamma, beta, mean_out, rstd_out, eps, Row_Size=cols)
+ * at online_best/infer.py:1063-1075 (kernel body online_best/infer.py:829-858):
+ *   mean = sum(x)/cols, var = sum((x - mean)^2)/cols, rstd = 1/sqrt(var + eps),
+ *   y = (x - mean) * rstd * gamma + beta      (fp32 arithmetic, one rounding to `dtype`)
+ *   x, y      [rows, cols] contiguous, element type `dtype` (y may alias x)
+ *   gamma     [cols], beta [cols], element type `param_dtype`
+ *   mean_out, rstd_out   fp32 [rows] or NULL
+ * Per-row results are deterministic (fixed reduction order).
+ */
+int cti_ebag_layernorm(const void* x, void* y, int64_t rows, int64_t cols, int32_t dtype,
+                       const void* gamma, const void* beta, int32_t param_dtype, float eps,
+                       float* mean_out, float* rstd_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@ CPU restatements of the fused sparse-feature embedding-bag path:
   to_global_offsets  the closed-form conversion reference layout -> offsets[S*B+1]
   merge_layouts      online_best/infer.py:581-631 (per-slot concatenation of sub-batches)
   merge_pair_layouts online_best/infer.py:2977-3037 (same, with its int32 round trip)
+  layer_norm_np      online_best/infer.py:829-858 (row LayerNorm of the pooled block, fp32)
   bf16 / fp16 encoders and decoders (IEEE round to nearest even)
 
 Table arrays: float32 arrays for 'f32'; uint16 bit patterns for 'bf16' and 'f16'.
@@ -310,3 +311,27 @@ def merge_pair_layouts(layouts, slot_num: int):
     int32 (.int() then .long(), :3008-3009 and :3019-3020), so ids >= 2**31 wrap."""
     v, o, vo = merge_layouts(layouts, slot_num)
     return v.astype(np.int32).astype(np.int64), o.astype(np.int32).astype(np.int64), vo
+
+
+# ------------------------------------------------------------------------------------------------
+# input LayerNorm of the pooled block
+# ------------------------------------------------------------------------------------------------
+def layer_norm_np(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float):
+    """Row LayerNorm, online_best/infer.py:829-858, in fp32.
+
+    x: float32 [rows, cols] (the pooled block decoded to fp32, :843); gamma, beta: float32 [cols].
+    mean = sum(x)/cols (:845); var = sum((x - mean)^2)/cols, two passes (:846-848);
+    rstd = 1/sqrt(var + eps) (:849); y = (x - mean) * rstd * gamma + beta (:856), each operation
+    rounded to fp32. The sums are taken in float64 and rounded once (the reference's reduction
+    order is not observable; the HIP kernel's is fixed), so comparisons use a tolerance.
+    Returns (y float32 [rows, cols], mean float32 [rows], rstd float32 [rows]).
+    """
+    x = np.asarray(x, np.float32)
+    n = np.float32(x.shape[1])
+    mean = (x.astype(np.float64).sum(axis=1).astype(np.float32) / n).astype(np.float32)
+    d = (x - mean[:, None]).astype(np.float32)
+    var = ((d.astype(np.float64) ** 2).sum(axis=1).astype(np.float32) / n).astype(np.float32)
+    rstd = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    y = ((d * rstd[:, None]).astype(np.float32) * np.asarray(gamma, np.float32)).astype(np.float32)
+    y = (y + np.asarray(beta, np.float32)).astype(np.float32)
+    return y, mean, rstd

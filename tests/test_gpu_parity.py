@@ -328,10 +328,15 @@ def test_rep_encoder_drop_in(pkg, dev):
         a, b = int(vo[s]), int(vo[s]) + int(ro[s * (case.B + 1) + case.B])
         slots[s + 1] = (torch.from_numpy(case.values[a:b]).to(dev), torch.from_numpy(ro[s * (case.B + 1):(s + 1) * (case.B + 1)]).to(dev))
     assert torch.equal(enc.pooled(slots), pooled)
+    # input LayerNorm on the HIP path (online_best/infer.py:1061-1076), then torch's Linear
+    g = enc.input_norm.weight.detach().cpu().numpy()
+    bta = enc.input_norm.bias.detach().cpu().numpy()
+    norm_ref, _, _ = orc.layer_norm_np(want, g, bta, enc.input_norm.eps)
+    np.testing.assert_allclose(enc.normalized(batch).cpu().numpy(), norm_ref, rtol=1e-5, atol=1e-5)
     y = enc(batch)
     ref = enc.linear(enc.input_norm(torch.from_numpy(want).to(dev)))
     assert y.shape == (case.B, 32)
-    torch.testing.assert_close(y, ref)
+    torch.testing.assert_close(y, ref, rtol=1e-4, atol=1e-4)
 
 
 # ---- device layout builders --------------------------------------------------------------------

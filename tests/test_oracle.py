@@ -292,3 +292,71 @@ def test_oracle_reproduces_golden_fixtures(path):
     got = orc.pool_c(fx["values"], fx["offsets"], fx["tables"], fx["table_dtype"], fx["pooling"],
                      fx["out_dtype"], batch=fx["batch"], val_base=fx.get("val_base"))
     assert np.array_equal(got, fx["expected"])
+
+
+# ---- input LayerNorm (online_best/infer.py:829-858) ----------------------------------------------
+def _ln_case(seed, rows=16, cols=448, offset=0.0, scale=1.0):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * scale + offset).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(cols)).astype(np.float32)
+    return x, g, b
+
+
+@pytest.mark.parametrize("cols", [7, 448, 3584])
+def test_layer_norm_matches_torch(cols):
+    x, g, b = _ln_case(cols, cols=cols)
+    y, mean, rstd = orc.layer_norm_np(x, g, b, 1e-5)
+    ref = Fn.layer_norm(torch.from_numpy(x).double(), (cols,), torch.from_numpy(g).double(),
+                        torch.from_numpy(b).double(), 1e-5).numpy()
+    np.testing.assert_allclose(y, ref, rtol=2e-5, atol=2e-5)
+    np.testing.assert_allclose(mean, x.astype(np.float64).mean(axis=1), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(rstd, 1 / np.sqrt(x.astype(np.float64).var(axis=1) + 1e-5), rtol=1e-5)
+
+
+def test_layer_norm_closed_forms():
+    # constant rows of exactly representable values: mean exact, deviations exactly 0, y == beta
+    cols = 256
+    x = np.repeat(np.array([[1.0], [-3.5], [0.0], [1024.0]], np.float32), cols, axis=1)
+    g = np.linspace(0.5, 2, cols).astype(np.float32)
+    b = np.linspace(-1, 1, cols).astype(np.float32)
+    y, mean, rstd = orc.layer_norm_np(x, g, b, 1e-5)
+    assert np.array_equal(mean, x[:, 0])
+    assert np.array_equal(y, np.broadcast_to(b, y.shape))
+    assert np.all(rstd == np.float32(1) / np.sqrt(np.float32(1e-5)))
+    # gamma = 1, beta = 0: every row has mean ~0 and variance var / (var + eps)
+    x, _, _ = _ln_case(3, rows=8, cols=1024, scale=3.0)
+    y, _, _ = orc.layer_norm_np(x, np.ones(1024, np.float32), np.zeros(1024, np.float32), 1e-5)
+    v = x.astype(np.float64).var(axis=1)
+    np.testing.assert_allclose(y.astype(np.float64).mean(axis=1), 0, atol=1e-6)
+    np.testing.assert_allclose(y.astype(np.float64).var(axis=1), v / (v + 1e-5), rtol=1e-5)
+
+
+def test_layer_norm_planted_mistakes_are_caught():
+    def torch_ref(x, g, b):
+        return Fn.layer_norm(torch.from_numpy(x).double(), (x.shape[1],), torch.from_numpy(g).double(),
+                             torch.from_numpy(b).double(), 1e-5).numpy()
+
+    # well-conditioned rows: unbiased variance (N-1) and a wrong eps are visible at 1e-4
+    x, g, b = _ln_case(8, rows=8, cols=64)
+    ref = torch_ref(x, g, b)
+    assert np.allclose(orc.layer_norm_np(x, g, b, 1e-5)[0], ref, rtol=1e-4, atol=1e-4)
+    mean = x.mean(axis=1, dtype=np.float64)[:, None]
+    v = x.var(axis=1, dtype=np.float64)[:, None]
+    unbiased = (x - mean) / np.sqrt(x.var(axis=1, ddof=1, dtype=np.float64)[:, None] + 1e-5) * g + b
+    wrong_eps = (x - mean) / np.sqrt(v + 1e-2) * g + b
+    for wrong in (unbiased, wrong_eps):
+        assert not np.allclose(wrong, ref, rtol=1e-4, atol=1e-4)
+
+    # large mean, small spread: the two-pass variance survives, a one-pass E[x^2] - E[x]^2 in fp32
+    # or skipping the centring does not (fp32 rounding of the mean alone costs ~3e-3 here)
+    x, g, b = _ln_case(9, rows=8, cols=512, offset=3000.0, scale=0.05)
+    ref = torch_ref(x, g, b)
+    assert np.allclose(orc.layer_norm_np(x, g, b, 1e-5)[0], ref, rtol=1e-2, atol=1e-2)
+    n = x.shape[1]
+    m32 = (x.sum(axis=1, dtype=np.float32) / np.float32(n)).astype(np.float32)[:, None]
+    one_pass_var = np.maximum((x * x).sum(axis=1, dtype=np.float32)[:, None] / np.float32(n) - m32 * m32, 0)
+    one_pass = (x - m32) / np.sqrt(one_pass_var + np.float32(1e-5)) * g + b
+    no_centre = x / np.sqrt(x.var(axis=1, dtype=np.float64)[:, None] + 1e-5) * g + b
+    for wrong in (one_pass, no_centre):
+        assert not np.allclose(wrong, ref, rtol=1e-2, atol=1e-2)
