@@ -6,6 +6,10 @@ B = 4096 samples, geometric(mean 8) bag lengths, Zipf(1.1) ids, mean pooling, bf
 are resident in HBM before timing; step k uses index set k mod n_sets, so consecutive steps do
 not find each other's rows in L2 / MALL.
 
+`--int8` row-quantises every table on the device first (online_best/infer.py:895-901) and pools
+the int8 rows with their fp32 scales (online_best/infer.py:904-942); the algorithmic bytes count
+1 byte per element plus the 4-byte scale of each looked-up row.
+
 `--stage layernorm` times the encoder's input LayerNorm instead (online_best/infer.py:1061-1076):
 the workload's batches are pooled once, and each step normalises one pooled block
 [B, sum(D)] (rows/s; roofline bytes = the block read and written plus gamma and beta).
@@ -154,6 +158,7 @@ def main():
     ap.add_argument("--block-threshold", type=int, default=0)
     ap.add_argument("--stage", default="pool", choices=["pool", "layernorm"],
                     help="time the pooling step (default) or the input LayerNorm over pooled blocks")
+    ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times (scales rocprofv3 FETCH/WRITE_SIZE) and exit")
     args = ap.parse_args()
@@ -191,13 +196,18 @@ def main():
     log("filling tables on the device")
     tables = W.make_tables(wl0, dev, seed=0)
     inputs = [W.to_device(wl, dev) for wl in wls]
-    plan = pkg.PooledEmbedding(tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype, long_threshold=args.long_threshold,
-                               use_bins=args.bins, block_threshold=args.block_threshold, max_batch=wl0.batch)
+    pooled_tables = tables
+    if args.int8:
+        log("quantising the tables to int8")
+        pooled_tables = [pkg.quantize_embedding_int8(t) for t in tables]
+    plan = pkg.PooledEmbedding(pooled_tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype,
+                               long_threshold=args.long_threshold, use_bins=args.bins,
+                               block_threshold=args.block_threshold, max_batch=wl0.batch)
     out = torch.empty((wl0.batch, sum(wl0.dims)), dtype=wl0.out_dtype, device=dev)
     if args.stage == "layernorm":
         return bench_layernorm(args, pkg, plan, inputs, wl0, dev)
-    bytes_alg = [wl.bytes_algorithmic() for wl in wls]
-    bytes_comp = [wl.bytes_compulsory() for wl in wls]
+    bytes_alg = [wl.bytes_algorithmic(int8=args.int8) for wl in wls]
+    bytes_comp = [wl.bytes_compulsory(int8=args.int8) for wl in wls]
     torch.cuda.synchronize()
 
     log(f"warmup {args.warmup} steps")
@@ -230,10 +240,24 @@ def main():
     log(f"{ms_per_step * 1e3:.1f} us/step wall, {mean_launch_s * 1e6:.1f} us/step on the GPU, "
         f"{achieved:.0f} GB/s algorithmic, {used_comp / mean_launch_s / 1e9:.0f} GB/s compulsory")
 
+    accuracy = None
+    if args.int8:
+        # int8 pooled rows against the same batch pooled from the float tables (fp32 output)
+        v, o = inputs[0]
+        ref = pkg.PooledEmbedding(tables, pooling=wl0.pooling, out_dtype=torch.float32)(v, o)
+        got = pkg.PooledEmbedding(pooled_tables, pooling=wl0.pooling, out_dtype=torch.float32)(v, o)
+        err = (got - ref).float()
+        accuracy = {"vs": "float tables, fp32 output, index set 1",
+                    "max_abs_err": err.abs().max().item(),
+                    "rel_rms_err": (err.pow(2).mean().sqrt() / ref.float().pow(2).mean().sqrt()).item()}
+        del ref, got, err
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
         cpu = cpu_baseline(wl0, tables, args.cpu_seconds)
+        if args.int8:
+            cpu["sample"] += " (the reference's CPU path has no int8 tables: this is its float loop)"
 
     rec = {
         "metric": METRIC,
@@ -246,19 +270,23 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {torch.bfloat16: "bf16", torch.float32: "f32", torch.float16: "f16"}[wl0.table_dtype],
-        "data": f"synthetic: {args.sets} seeded index sets rotated, random N(0, 0.01) tables",
+        "dtype": "i8" if args.int8 else {torch.bfloat16: "bf16", torch.float32: "f32",
+                                          torch.float16: "f16"}[wl0.table_dtype],
+        "data": f"synthetic: {args.sets} seeded index sets rotated, random N(0, 0.01) tables"
+                + (", row-quantised to int8 on the device" if args.int8 else ""),
         "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}", "batch": wl0.batch,
                    "fields": wl0.num_fields, "dims": sorted(set(wl0.dims)), "pooling": wl0.pooling,
                    "nnz_mean": float(np.mean([wl.nnz for wl in wls])), "index_sets": args.sets,
-                   "length_binning": bool(args.bins)},
+                   "length_binning": bool(args.bins), "int8_tables": bool(args.int8)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profiles(args.workload),
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_from_profiles(args.workload + ("-int8" if args.int8 else "")),
                      "kernel": "pool_kernel" if not args.bins else "bin_kernel + pool_kernel + pool_long_kernel",
                      "bytes_per_launch": used_bytes,
                      "compulsory_bytes_per_launch": used_comp, "launch_us_mean": mean_launch_s * 1e6},
         "cpu_baseline": cpu,
     }
+    if accuracy is not None:
+        rec["int8_accuracy"] = accuracy
     print(json.dumps(rec), flush=True)
 
 

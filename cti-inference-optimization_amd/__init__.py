@@ -3,6 +3,8 @@
 Public surface:
   fused_all_slots_embedding  drop-in for the reference's fused_all_slots_embedding_kernel launch
   fused_embedding            the RepEncoder.forward fused step on a flat-layout batch dict
+  quantize_embedding_int8    int8 row quantisation of a table (int8 rows + fp32 row scales)
+  fused_all_slots_embedding_int8   drop-in for the reference's int8 fused kernel launch
   embedding_bag_pooled       per-field tables, global offsets, sum/mean, chosen output dtype
   PooledEmbedding            the same with the table descriptors prepared once (serving loops)
   layer_norm                 the encoder's input LayerNorm over the pooled rows
@@ -14,7 +16,8 @@ from . import workloads
 from ._capi import EbagError, lib as load_library
 from .encoder import RepEncoder
 from .layout import collate_flat_layout, merge_batches, pack_slots, prebuild_flat_layout
-from .ops import PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_embedding, layer_norm
+from .ops import (PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_all_slots_embedding_int8,
+                  fused_embedding, layer_norm, quantize_embedding_int8)
 
 __all__ = [
     "EbagError",
@@ -28,6 +31,8 @@ __all__ = [
     "PooledEmbedding",
     "fused_all_slots_embedding",
     "fused_embedding",
+    "fused_all_slots_embedding_int8",
+    "quantize_embedding_int8",
     "layer_norm",
     "workloads",
 ]

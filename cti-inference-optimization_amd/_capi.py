@@ -17,9 +17,9 @@ import torch  # noqa: F401  (must precede the dlopen below, see module docstring
 LIB_NAME = "libcti_ebag.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
-F32, BF16, F16 = 0, 1, 2
+F32, BF16, F16, I8 = 0, 1, 2, 3
 I64, I32 = 0, 1
 SUM, MEAN = 0, 1
 
@@ -51,6 +51,7 @@ class Table(ctypes.Structure):
         ("row_stride", ctypes.c_int64),
         ("dim", ctypes.c_int32),
         ("out_col", ctypes.c_int32),
+        ("row_scale", ctypes.c_void_p),
     ]
 
 
@@ -92,6 +93,11 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _I64, _I64, _I32, _P, _P, _I32, ctypes.c_float, _P, _P, _P],
     ),
+    "cti_ebag_fused_all_slots_int8": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, _I32, _I64, _I32, _I32, _I64, _I64, _P],
+    ),
+    "cti_ebag_quantize_int8": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _P]),
 }
 
 _lib = None

@@ -18,6 +18,10 @@ struct bf16_t {
 struct f16_t {
   uint16_t bits;
 };
+// int8 row-quantised table element; a row's value is q * row_scale[row] (fp32 scale per row).
+struct i8_t {
+  int8_t q;
+};
 
 // bf16 -> fp32 is exact: the bf16 word is the high half of the fp32 word.
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
@@ -34,11 +38,13 @@ struct Elem;
 template <>
 struct Elem<float> {
   static constexpr int kBytes = 4;
+  static constexpr int kVecBytes = 16;  // bytes of one lane's row vector
   __device__ static __forceinline__ float load(const void* p) { return *static_cast<const float*>(p); }
 };
 template <>
 struct Elem<bf16_t> {
   static constexpr int kBytes = 2;
+  static constexpr int kVecBytes = 16;  // bytes of one lane's row vector
   __device__ static __forceinline__ float load(const void* p) {
     return bf16_bits_to_f32(*static_cast<const uint16_t*>(p));
   }
@@ -46,9 +52,28 @@ struct Elem<bf16_t> {
 template <>
 struct Elem<f16_t> {
   static constexpr int kBytes = 2;
+  static constexpr int kVecBytes = 16;  // bytes of one lane's row vector
   __device__ static __forceinline__ float load(const void* p) {
     return f16_bits_to_f32(*static_cast<const uint16_t*>(p));
   }
+};
+template <>
+struct Elem<i8_t> {
+  static constexpr int kBytes = 1;
+  static constexpr int kVecBytes = 8;  // 8 elements per lane, as many as a 16-byte bf16 vector
+  __device__ static __forceinline__ float load(const void* p) {  // unscaled q
+    return static_cast<float>(*static_cast<const int8_t*>(p));
+  }
+};
+
+// Whether rows of a table type carry a per-row scale.
+template <typename T>
+struct Quantized {
+  static constexpr bool value = false;
+};
+template <>
+struct Quantized<i8_t> {
+  static constexpr bool value = true;
 };
 
 // Add the elements held in one 16-byte vector to fp32 accumulators, in element order.
@@ -75,6 +100,26 @@ __device__ __forceinline__ void acc16(float* a, const uint4& v, f16_t) {
     a[2 * i] += f16_bits_to_f32(w[i] & 0xffffu);
     a[2 * i + 1] += f16_bits_to_f32(w[i] >> 16);
   }
+}
+// int8 rows: a[k] = fma(q_k, scale, a[k]) in element order (one rounding per element, as the
+// reference's `acc += int8_row * scale_val` compiles to).
+// int8 rows: the 8 elements in v.x, v.y, each a = fma(q, s, a) in element order.
+__device__ __forceinline__ void acc8_scaled(float* a, const uint4& v, float s) {
+  const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      a[4 * i + k] = __builtin_fmaf(static_cast<float>(static_cast<int8_t>(w[i] >> (8 * k))), s, a[4 * i + k]);
+  }
+}
+
+// One lane vector of a row (Elem<TT>::kVecBytes bytes) into the accumulators; `s` is the row's
+// scale (quantized tables).
+template <typename TT>
+__device__ __forceinline__ void acc_row(float* a, const uint4& v, float s) {
+  if constexpr (Quantized<TT>::value) acc8_scaled(a, v, s);
+  else acc16(a, v, TT{});
 }
 
 // Store N fp32 values as output type OT (N * sizeof(OT) is a multiple of 8 bytes and the

@@ -20,6 +20,7 @@ inline int dtype_bytes(int32_t dt) {
     case CTI_EBAG_F32: return 4;
     case CTI_EBAG_BF16: return 2;
     case CTI_EBAG_F16: return 2;
+    case CTI_EBAG_I8: return 1;
     default: return 0;
   }
 }

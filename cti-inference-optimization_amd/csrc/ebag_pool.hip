@@ -3,13 +3,15 @@
 // Semantics follow the reference kernel online_best/infer.py:805-827 and the per-field oracle
 // loop baseline/infer.py:256-263:
 //   out[b, col_f + d] = pool_{i in bag(f, b)} table_f[clamp(values[i], 0, rows_f - 1), d]
-// with fp32 accumulation, empty bag -> 0, and one rounding to the output type.
+// with fp32 accumulation, empty bag -> 0, and one rounding to the output type. int8 tables
+// (online_best/infer.py:904-942) accumulate acc = fma(q, row_scale[row], acc) in element order.
 //
 // This is a gather (no matrix cores); on MI355X it is bound by vector-ALU issue and memory latency
 // more than by HBM bandwidth, so the design keeps VALU work per pooled row small. Decomposition:
-//   * A row of D elements is read as 16-byte vectors by LANES = row_bytes/16 lanes, so a 64-lane
-//     wavefront holds R = 64/LANES lane groups ("subgroups"). For D = 128 bf16: 16 lanes x 16 B
-//     per row, 4 subgroups per wavefront.
+//   * A row of D elements is read as lane vectors (16 bytes; 8 bytes for int8, so a lane holds
+//     8 elements either way) by LANES = row_bytes / vector bytes lanes, so a 64-lane wavefront
+//     holds R = 64/LANES lane groups ("subgroups"). For D = 128 bf16: 16 lanes x 16 B per row,
+//     4 subgroups per wavefront; D = 128 int8: 16 lanes x 8 B.
 //   * Main kernel: one wavefront per workgroup, one tile of ROUNDS * R consecutive bags of one
 //     field. The tile's short bags are ranked by length and pooled R at a time, one bag per
 //     subgroup, so the bags pooled side by side need about the same number of steps:
@@ -38,7 +40,7 @@
 //     `count`; the long kernel reads `total`. A call therefore leaves `count` at zero for the next.
 //   * Tiles are renumbered so each of the 8 XCDs (own L2 each) works on a contiguous range of
 //     tiles, i.e. on a few fields at a time.
-//   * Rows that are not whole 16-byte vectors, or misaligned buffers, use an element-wise kernel
+//   * Rows that are not whole lane vectors, or misaligned buffers, use an element-wise kernel
 //     (one wavefront per bag, element order, never split).
 // All kernels write disjoint output rows and combine partial sums in a fixed order, so results
 // are deterministic run to run.
@@ -55,7 +57,7 @@ namespace {
 
 // Tuning knobs (compile-time). Defaults are the measured best on MI355X for D=128 bf16.
 #ifndef CTI_EBAG_ROWS_IN_FLIGHT
-#define CTI_EBAG_ROWS_IN_FLIGHT 4  // 16-byte row loads in flight per lane before they are consumed
+#define CTI_EBAG_ROWS_IN_FLIGHT 4  // row vector loads in flight per lane before they are consumed
 #endif
 #ifndef CTI_EBAG_XCD_REMAP
 #define CTI_EBAG_XCD_REMAP 1  // give each XCD a contiguous range of tiles
@@ -83,8 +85,19 @@ __device__ __forceinline__ uint4 load_row16(const char* p) {
 #endif
 }
 
+// One lane's row vector (Elem<TT>::kVecBytes bytes; an 8-byte vector fills .x and .y).
+template <typename TT>
+__device__ __forceinline__ uint4 load_row_vec(const char* p) {
+  if constexpr (Elem<TT>::kVecBytes == 16) {
+    return load_row16(p);
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    return make_uint4(v.x, v.y, 0u, 0u);
+  }
+}
+
 enum Variant : int {
-  kVarL1 = 0,  // LANES = 1 << v, one 16-byte vector per lane, for v = 0..6
+  kVarL1 = 0,  // LANES = 1 << v, one lane vector per lane, for v = 0..6
   kVarL64V2 = 7,
   kVarL64V4 = 8,
   kVarGeneric = 9,
@@ -93,6 +106,7 @@ enum Variant : int {
 
 struct FieldDesc {
   const char* table;   // row 0 of the field's table
+  const float* row_scale;  // per-row scale of an int8 table (NULL otherwise)
   int64_t max_row;     // rows - 1 (clamp bound)
   int64_t row_bytes;   // byte distance between consecutive rows
   int32_t dim;         // columns pooled
@@ -148,7 +162,6 @@ __device__ __forceinline__ int block_tile() {
 
 // Buffer resource over one table: 32-bit byte offsets, offsets at or past the span read as zeros.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
-constexpr unsigned int kOutOfRange = 0xfffffff0u;  // above every span accepted by the host
 __device__ __forceinline__ Rsrc make_rsrc(const char* base, uint32_t span) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), static_cast<short>(0), static_cast<int>(span),
                                            0x00020000);  // raw buffer, 32-bit data format
@@ -157,6 +170,19 @@ __device__ __forceinline__ uint4 buffer_load16(Rsrc r, unsigned int off) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <typename TT>
+__device__ __forceinline__ uint4 buffer_load_vec(Rsrc r, unsigned int off) {
+  if constexpr (Elem<TT>::kVecBytes == 16) {
+    return buffer_load16(r, off);
+  } else {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint4(v.x, v.y, 0u, 0u);
+  }
+}
+__device__ __forceinline__ float buffer_load_f32(Rsrc r, unsigned int off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
 __device__ __forceinline__ int64_t load_index(const PoolParams& p, int64_t e) {
@@ -176,7 +202,8 @@ __device__ __forceinline__ void bag_range(const PoolParams& p, int gidx, int64_t
 template <typename TT, int LANES, int VPL>
 struct Shape {
   static constexpr int R = kWave / LANES;            // subgroups per wavefront
-  static constexpr int VEC = 16 / Elem<TT>::kBytes;  // elements per 16-byte vector
+  static constexpr int VB = Elem<TT>::kVecBytes;     // bytes per lane vector
+  static constexpr int VEC = VB / Elem<TT>::kBytes;  // elements per lane vector
   static constexpr int NACC = VPL * VEC;             // fp32 accumulators per lane
   static constexpr int D = LANES * NACC;             // row width
   static constexpr int U0 = CTI_EBAG_ROWS_IN_FLIGHT / VPL > 0 ? CTI_EBAG_ROWS_IN_FLIGHT / VPL : 1;
@@ -188,9 +215,9 @@ struct Shape {
 // wavefront's private 64-entry LDS slice for row ids: its accesses are ordered by program order
 // within the wavefront, so no workgroup barrier is involved.
 template <typename TT, int LANES, int VPL>
-__device__ __forceinline__ void wave_slice_partial(const PoolParams& p, const char* table, int64_t max_row,
-                                                   int64_t row_bytes, int64_t s0, int64_t s1, float* pa,
-                                                   unsigned int* ids) {
+__device__ __forceinline__ void wave_slice_partial(const PoolParams& p, const char* table, const float* row_scale,
+                                                   int64_t max_row, int64_t row_bytes, int64_t s0, int64_t s1,
+                                                   float* pa, unsigned int* ids) {
   using S = Shape<TT, LANES, VPL>;
   const int lane = lane_id();
   const int g = lane / LANES, sl = lane % LANES;
@@ -199,6 +226,7 @@ __device__ __forceinline__ void wave_slice_partial(const PoolParams& p, const ch
     const int n = static_cast<int>(s1 - c < kWave ? s1 - c : kWave);
     for (int k = 0; k < n; k += S::U * S::R) {
       uint4 v[S::U][VPL];
+      float sc[S::U];
 #pragma unroll
       for (int u = 0; u < S::U; ++u) {
         const int e = k + u * S::R + g;  // < 64 because U * R <= 64
@@ -206,12 +234,14 @@ __device__ __forceinline__ void wave_slice_partial(const PoolParams& p, const ch
         const bool act = e < n;
 #pragma unroll
         for (int q = 0; q < VPL; ++q)
-          v[u][q] = act ? load_row16(row + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
+          v[u][q] = act ? load_row_vec<TT>(row + (q * LANES + sl) * S::VB) : make_uint4(0u, 0u, 0u, 0u);
+        sc[u] = 1.f;
+        if constexpr (Quantized<TT>::value) sc[u] = act ? row_scale[ids[e]] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < S::U; ++u) {
 #pragma unroll
-        for (int q = 0; q < VPL; ++q) acc16(pa + q * S::VEC, v[u][q], TT{});
+        for (int q = 0; q < VPL; ++q) acc_row<TT>(pa + q * S::VEC, v[u][q], sc[u]);
       }
     }
   }
@@ -239,8 +269,9 @@ __device__ __forceinline__ void store_bag(const PoolParams& p, int64_t b, int ou
 // U row loads of one step: elements k .. k+U-1 of this subgroup's current chunk, whose row ids
 // are in `ids` (the subgroup's slice of the wavefront's LDS row-id buffer; immediate offsets).
 template <typename TT, int LANES, int VPL>
-__device__ __forceinline__ void load_step(const char* table, int64_t row_bytes, const unsigned int* ids, int sl,
-                                          int k, int live, uint4 (&v)[Shape<TT, LANES, VPL>::U][VPL]) {
+__device__ __forceinline__ void load_step(const char* table, const float* row_scale, int64_t row_bytes,
+                                          const unsigned int* ids, int sl, int k, int live,
+                                          uint4 (&v)[Shape<TT, LANES, VPL>::U][VPL], float (&sc)[Shape<TT, LANES, VPL>::U]) {
   using S = Shape<TT, LANES, VPL>;
 #pragma unroll
   for (int u = 0; u < S::U; ++u) {
@@ -249,17 +280,20 @@ __device__ __forceinline__ void load_step(const char* table, int64_t row_bytes, 
     const bool act = k + u < live;
 #pragma unroll
     for (int q = 0; q < VPL; ++q)
-      v[u][q] = act ? load_row16(row + (q * LANES + sl) * 16) : make_uint4(0u, 0u, 0u, 0u);
+      v[u][q] = act ? load_row_vec<TT>(row + (q * LANES + sl) * S::VB) : make_uint4(0u, 0u, 0u, 0u);
+    sc[u] = 1.f;
+    if constexpr (Quantized<TT>::value) sc[u] = act ? row_scale[r] : 0.f;
   }
 }
 
 template <typename TT, int LANES, int VPL>
-__device__ __forceinline__ void add_step(float* acc, const uint4 (&v)[Shape<TT, LANES, VPL>::U][VPL]) {
+__device__ __forceinline__ void add_step(float* acc, const uint4 (&v)[Shape<TT, LANES, VPL>::U][VPL],
+                                         const float (&sc)[Shape<TT, LANES, VPL>::U]) {
   using S = Shape<TT, LANES, VPL>;
 #pragma unroll
   for (int u = 0; u < S::U; ++u) {
 #pragma unroll
-    for (int q = 0; q < VPL; ++q) acc16(acc + q * S::VEC, v[u][q], TT{});
+    for (int q = 0; q < VPL; ++q) acc_row<TT>(acc + q * S::VEC, v[u][q], sc[u]);
   }
 }
 
@@ -302,8 +336,17 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLds
   const int64_t row_bytes = p.f[fi].row_bytes;
   const int gidx = p.f[fi].gidx;
   const int out_col = p.f[fi].out_col;
+  const float* const row_scale = p.f[fi].row_scale;
   const Rsrc rsrc = make_rsrc(table, BUF ? p.f[fi].span_bytes : 0u);
+  // int8 tables: the row scales, read alongside the rows (out-of-range offsets read as 0)
+  const Rsrc srsrc = make_rsrc(reinterpret_cast<const char*>(row_scale),
+                               BUF && Quantized<TT>::value ? static_cast<uint32_t>((max_row + 1) * 4) : 0u);
   const unsigned int shift = static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(row_bytes)));
+  // Row id staged for the slots past a bag's end: its row offset (2^32 - row_bytes, plus the
+  // lane's column offset) and its scale offset both lie past the buffers' ends (the host admits
+  // a table to the buffer path only if (rows + 1) * row_bytes <= 2^32), so those loads return
+  // zeros without a memory request and the steps need no per-row test.
+  const unsigned int r_pad = BUF ? 0xffffffffu >> shift : 0u;
 
   const int lane = lane_id();
   const int g = lane / LANES;   // subgroup inside the wavefront
@@ -344,29 +387,32 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLds
     for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
     for (int c = 0; __ballot(c < Lb) != 0; c += LANES) {
       __syncthreads();  // orders this chunk's LDS writes after the last reads
-      s.ids[lane] = c + sl < Lb ? static_cast<unsigned int>(clamp_i64(load_index(p, bs + c + sl), 0, max_row)) : 0u;
+      s.ids[lane] = c + sl < Lb ? static_cast<unsigned int>(clamp_i64(load_index(p, bs + c + sl), 0, max_row)) : r_pad;
       __syncthreads();
       const int live = Lb - c < LANES ? Lb - c : LANES;
       for (int k = 0; k < LANES; k += U) {
         if (__ballot(k < live) == 0) break;
         uint4 v[U][VPL];
+        float sc[U];
         if constexpr (BUF) {
-          // all U ids first, then branch-free loads (out-of-range offsets read as zeros)
+          // all U ids first, then branch-free loads (slots past the bag's end hold r_pad)
           unsigned int r[U];
 #pragma unroll
           for (int u = 0; u < U; ++u) r[u] = s.ids[g * LANES + k + u];
-          const unsigned int lane_off = static_cast<unsigned int>(sl * 16);
+          const unsigned int lane_off = static_cast<unsigned int>(sl * S::VB);
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             const unsigned int o = (r[u] << shift) + lane_off;
 #pragma unroll
-            for (int q = 0; q < VPL; ++q) v[u][q] = buffer_load16(rsrc, k + u < live ? o + q * LANES * 16 : kOutOfRange);
+            for (int q = 0; q < VPL; ++q) v[u][q] = buffer_load_vec<TT>(rsrc, o + q * LANES * S::VB);
+            sc[u] = 1.f;
+            if constexpr (Quantized<TT>::value) sc[u] = buffer_load_f32(srsrc, r[u] * 4u);
           }
           __builtin_amdgcn_sched_barrier(0);  // issue every load of the step before consuming any
         } else {
-          load_step<TT, LANES, VPL>(table, row_bytes, s.ids + g * LANES, sl, k, live, v);
+          load_step<TT, LANES, VPL>(table, row_scale, row_bytes, s.ids + g * LANES, sl, k, live, v, sc);
         }
-        add_step<TT, LANES, VPL>(acc, v);
+        add_step<TT, LANES, VPL>(acc, v, sc);
       }
     }
     if (has) store_bag<TT, OT, LANES, VPL>(p, b0 + bi, out_col, Lb, acc);
@@ -380,7 +426,7 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLds
 #pragma unroll
     for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
     __syncthreads();
-    wave_slice_partial<TT, LANES, VPL>(p, table, max_row, row_bytes, bs, be, pa, s.ids);
+    wave_slice_partial<TT, LANES, VPL>(p, table, row_scale, max_row, row_bytes, bs, be, pa, s.ids);
     if (g == 0) store_bag<TT, OT, LANES, VPL>(p, b0 + src, out_col, be - bs, pa);
   }
 }
@@ -446,8 +492,8 @@ __global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams 
     float pa[S::NACC];
 #pragma unroll
     for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
-    wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].max_row, p.f[fi].row_bytes, s0, s1, pa,
-                                       s_ids + wave * kWave);
+    wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].row_scale, p.f[fi].max_row, p.f[fi].row_bytes, s0,
+                                       s1, pa, s_ids + wave * kWave);
     if (g == 0) {
 #pragma unroll
       for (int q = 0; q < VPL; ++q) {
@@ -476,7 +522,7 @@ __global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams 
 }
 
 // Element-wise kernel for any row width / alignment: one wavefront per bag, rows accumulated in
-// order, 4 columns per lane per pass.
+// order, 4 columns per lane per pass (int8 rows: fma with the row's scale).
 template <typename TT, typename OT>
 __global__ void __launch_bounds__(kMainThreads) pool_generic_kernel(const PoolParams p) {
   constexpr int NC = 4;
@@ -500,14 +546,24 @@ __global__ void __launch_bounds__(kMainThreads) pool_generic_kernel(const PoolPa
     for (int i = 0; i < NC; ++i) acc[i] = 0.f;
     for (int64_t c = start; c < end; c += kWave) {
       int64_t roff = 0;
-      if (c + lane < end) roff = clamp_i64(load_index(p, c + lane), 0, max_row) * row_bytes;
+      float rsc = 0.f;
+      if (c + lane < end) {
+        const int64_t row = clamp_i64(load_index(p, c + lane), 0, max_row);
+        roff = row * row_bytes;
+        if constexpr (Quantized<TT>::value) rsc = p.f[fi].row_scale[row];
+      }
       const int n = static_cast<int>(end - c < kWave ? end - c : kWave);
       for (int k = 0; k < n; ++k) {
         const int64_t ro = shfl_i64(roff, k);
+        const float sk = Quantized<TT>::value ? __int_as_float(shfl_i32(__float_as_int(rsc), k)) : 1.f;
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
           const int col = c0 + i * kWave + lane;
-          if (col < dim) acc[i] += Elem<TT>::load(table + ro + static_cast<int64_t>(col) * Elem<TT>::kBytes);
+          if (col < dim) {
+            const float x = Elem<TT>::load(table + ro + static_cast<int64_t>(col) * Elem<TT>::kBytes);
+            if constexpr (Quantized<TT>::value) acc[i] = __builtin_fmaf(x, sk, acc[i]);
+            else acc[i] += x;
+          }
         }
       }
     }
@@ -549,14 +605,15 @@ constexpr int64_t kMaxShortBag = int64_t{1} << 24;
 
 int pick_variant(const cti_ebag_table& t, int tb, int ob, const void* out, int64_t out_row_stride) {
   const int64_t row_bytes = static_cast<int64_t>(t.dim) * tb;
-  const bool table_ok = (reinterpret_cast<uintptr_t>(t.data) % 16 == 0) && ((t.row_stride * tb) % 16 == 0);
-  const int vec = 16 / tb;
+  const int vb = tb == 1 ? 8 : 16;  // lane vector bytes (Elem<TT>::kVecBytes; only int8 has 1-byte elements)
+  const bool table_ok = (reinterpret_cast<uintptr_t>(t.data) % vb == 0) && ((t.row_stride * tb) % vb == 0);
+  const int vec = vb / tb;
   const int align = vec * ob < 16 ? vec * ob : 16;
   const bool out_ok = (reinterpret_cast<uintptr_t>(out) % align == 0) &&
                       ((out_row_stride * ob) % align == 0) &&
                       ((static_cast<int64_t>(t.out_col) * ob) % align == 0);
-  if (!table_ok || !out_ok || row_bytes % 16 != 0) return kVarGeneric;
-  const int64_t nvec = row_bytes / 16;
+  if (!table_ok || !out_ok || row_bytes % vb != 0) return kVarGeneric;
+  const int64_t nvec = row_bytes / vb;
   for (int v = 0; v <= 6; ++v) {
     if (nvec == (int64_t{1} << v)) return v;
   }
@@ -616,7 +673,10 @@ hipError_t launch_typed(int tdt, int odt, int variant, const PoolParams& p, cons
     case CTI_EBAG_BF16 * 3 + CTI_EBAG_F16: return launch_variant<bf16_t, f16_t>(variant, p, l, s);
     case CTI_EBAG_F16 * 3 + CTI_EBAG_F32: return launch_variant<f16_t, float>(variant, p, l, s);
     case CTI_EBAG_F16 * 3 + CTI_EBAG_BF16: return launch_variant<f16_t, bf16_t>(variant, p, l, s);
-    default: return launch_variant<f16_t, f16_t>(variant, p, l, s);
+    case CTI_EBAG_F16 * 3 + CTI_EBAG_F16: return launch_variant<f16_t, f16_t>(variant, p, l, s);
+    case CTI_EBAG_I8 * 3 + CTI_EBAG_F32: return launch_variant<i8_t, float>(variant, p, l, s);
+    case CTI_EBAG_I8 * 3 + CTI_EBAG_BF16: return launch_variant<i8_t, bf16_t>(variant, p, l, s);
+    default: return launch_variant<i8_t, f16_t>(variant, p, l, s);
   }
 }
 
@@ -653,6 +713,7 @@ int validate_tables(const Job& j) {
     if (t.out_col < 0 || static_cast<int64_t>(t.out_col) + t.dim > j.out_row_stride)
       return set_error(CTI_EBAG_EINVAL, "table %d: columns [%d, %lld) fall outside the output row of %lld", f, t.out_col,
                        (long long)t.out_col + t.dim, (long long)j.out_row_stride);
+    if (j.tdt == CTI_EBAG_I8 && !t.row_scale) return set_error(CTI_EBAG_EINVAL, "table %d: int8 table without row_scale", f);
   }
   return CTI_EBAG_OK;
 }
@@ -710,6 +771,7 @@ int run_job(const Job& j, hipStream_t stream) {
         const cti_ebag_table& t = j.tables[f];
         FieldDesc& d = p.f[i];
         d.table = static_cast<const char*>(t.data);
+        d.row_scale = j.tdt == CTI_EBAG_I8 ? t.row_scale : nullptr;
         d.max_row = t.rows - 1;
         d.row_bytes = t.row_stride * tb;
         d.dim = t.dim;
@@ -717,7 +779,10 @@ int run_job(const Job& j, hipStream_t stream) {
         d.gidx = f;
         const int64_t span = (t.rows - 1) * d.row_bytes + static_cast<int64_t>(t.dim) * tb;
         const bool pow2 = (d.row_bytes & (d.row_bytes - 1)) == 0;
-        d.span_bytes = pow2 && span < static_cast<int64_t>(kOutOfRange) ? static_cast<uint32_t>(span) : 0u;
+        // buffer path: power-of-two rows of >= 8 bytes and (rows + 1) * row_bytes <= 2^32, so the
+        // pad row id 0xffffffff >> log2(row_bytes) addresses past both the rows and the scales
+        const bool fits = d.row_bytes >= 8 && t.rows < (int64_t{1} << 32) / d.row_bytes;
+        d.span_bytes = pow2 && fits ? static_cast<uint32_t>(span) : 0u;
         all_buf = all_buf && d.span_bytes != 0;
       }
       p.buffer_ok = all_buf ? 1 : 0;
@@ -742,21 +807,23 @@ int64_t workspace_bytes(int64_t batch, int32_t num_fields) {
 
 using namespace cti;
 
-extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* val_offsets,
-                                        const int64_t* row_offsets, const void* weight, int32_t dtype,
-                                        void* out, int64_t batch_size, int32_t num_slots, int32_t emb_dim,
-                                        int64_t max_idx, int64_t nnz, void* stream) {
-  clear_error();
+namespace cti {
+namespace {
+
+// The reference-layout launch (one shared table, slot-local offsets, sum pooling) for any table
+// type; `scale` is the int8 table's per-row scale.
+int run_all_slots(const int64_t* values, const int64_t* val_offsets, const int64_t* row_offsets, const void* weight,
+                  const float* scale, int32_t tdt, void* out, int32_t odt, int64_t batch_size, int32_t num_slots,
+                  int32_t emb_dim, int64_t max_idx, int64_t nnz, void* stream) {
   if (batch_size < 0) return set_error(CTI_EBAG_EINVAL, "batch_size must be >= 0 (got %lld)", (long long)batch_size);
   if (num_slots < 0) return set_error(CTI_EBAG_EINVAL, "num_slots must be >= 0 (got %d)", num_slots);
   if (emb_dim < 1) return set_error(CTI_EBAG_EINVAL, "emb_dim must be >= 1 (got %d)", emb_dim);
   if (max_idx < 0) return set_error(CTI_EBAG_EINVAL, "max_idx must be >= 0 (got %lld)", (long long)max_idx);
   if (max_idx >= INT32_MAX) return set_error(CTI_EBAG_EUNSUPPORTED, "max_idx must be < 2^31 - 1 (got %lld)", (long long)max_idx);
   if (nnz < 0) return set_error(CTI_EBAG_EINVAL, "nnz must be >= 0 (got %lld)", (long long)nnz);
-  if (!dtype_ok(dtype)) return set_error(CTI_EBAG_EINVAL, "unknown dtype code %d", dtype);
   if (batch_size == 0 || num_slots == 0) return CTI_EBAG_OK;
-  if (!val_offsets || !row_offsets || !weight || !out || (nnz > 0 && !values))
-    return set_error(CTI_EBAG_EINVAL, "NULL device pointer among values/val_offsets/row_offsets/weight/out");
+  if (!val_offsets || !row_offsets || !weight || !out || (nnz > 0 && !values) || (tdt == CTI_EBAG_I8 && !scale))
+    return set_error(CTI_EBAG_EINVAL, "NULL device pointer among values/val_offsets/row_offsets/weight/scale/out");
   std::vector<cti_ebag_table> tables(num_slots);
   for (int s = 0; s < num_slots; ++s) {
     tables[s].data = weight;
@@ -764,6 +831,7 @@ extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* va
     tables[s].row_stride = emb_dim;
     tables[s].dim = emb_dim;
     tables[s].out_col = s * emb_dim;
+    tables[s].row_scale = scale;
   }
   Job j;
   memset(&j, 0, sizeof(j));
@@ -775,12 +843,36 @@ extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* va
   j.batch = batch_size;
   j.num_fields = num_slots;
   j.tables = tables.data();
-  j.tdt = dtype;
+  j.tdt = tdt;
   j.pooling = CTI_EBAG_SUM;
   j.out = out;
-  j.odt = dtype;
+  j.odt = odt;
   j.out_row_stride = static_cast<int64_t>(num_slots) * emb_dim;
   return run_job(j, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+}  // namespace cti
+
+extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* val_offsets,
+                                        const int64_t* row_offsets, const void* weight, int32_t dtype,
+                                        void* out, int64_t batch_size, int32_t num_slots, int32_t emb_dim,
+                                        int64_t max_idx, int64_t nnz, void* stream) {
+  clear_error();
+  if (!dtype_ok(dtype)) return set_error(CTI_EBAG_EINVAL, "unknown dtype code %d", dtype);
+  return run_all_slots(values, val_offsets, row_offsets, weight, nullptr, dtype, out, dtype, batch_size, num_slots,
+                       emb_dim, max_idx, nnz, stream);
+}
+
+extern "C" int cti_ebag_fused_all_slots_int8(const int64_t* values, const int64_t* val_offsets,
+                                             const int64_t* row_offsets, const int8_t* weight_int8,
+                                             const float* scale, void* out, int32_t out_dtype, int64_t batch_size,
+                                             int32_t num_slots, int32_t emb_dim, int64_t max_idx, int64_t nnz,
+                                             void* stream) {
+  clear_error();
+  if (!dtype_ok(out_dtype)) return set_error(CTI_EBAG_EINVAL, "unknown output dtype code %d", out_dtype);
+  return run_all_slots(values, val_offsets, row_offsets, weight_int8, scale, CTI_EBAG_I8, out, out_dtype, batch_size,
+                       num_slots, emb_dim, max_idx, nnz, stream);
 }
 
 extern "C" int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fields) {
@@ -796,7 +888,8 @@ extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t 
   clear_error();
   if (index_type != CTI_EBAG_I64 && index_type != CTI_EBAG_I32)
     return set_error(CTI_EBAG_EINVAL, "unknown index type code %d", index_type);
-  if (!dtype_ok(table_dtype)) return set_error(CTI_EBAG_EINVAL, "unknown table dtype code %d", table_dtype);
+  if (!dtype_ok(table_dtype) && table_dtype != CTI_EBAG_I8)
+    return set_error(CTI_EBAG_EINVAL, "unknown table dtype code %d", table_dtype);
   if (!dtype_ok(out_dtype)) return set_error(CTI_EBAG_EINVAL, "unknown output dtype code %d", out_dtype);
   if (pooling != CTI_EBAG_SUM && pooling != CTI_EBAG_MEAN) return set_error(CTI_EBAG_EINVAL, "unknown pooling code %d", pooling);
   if (nnz < 0) return set_error(CTI_EBAG_EINVAL, "nnz must be >= 0 (got %lld)", (long long)nnz);

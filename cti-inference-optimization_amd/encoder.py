@@ -7,6 +7,10 @@ the ``input_norm`` parameters (the reference's Triton LayerNorm, online_best/inf
 and ``linear`` (torch's Linear, a plain library GEMM) maps them to d_model
 (online_best/infer.py:1084). Like the reference's Triton kernels, the pooling and the
 LayerNorm are forward-only (inference).
+
+``quantize_int8_()`` is the reference's int8 switch (``_USE_INT8_EMB``, online_best/infer.py:893
+and :976-1026): the table is row-quantised once on the device and every later ``pooled`` reads
+the int8 rows and their fp32 scales; ``dequantize_()`` switches back to the float table.
 """
 from __future__ import annotations
 
@@ -14,7 +18,7 @@ import torch
 from torch import nn
 
 from .layout import pack_slots
-from .ops import fused_all_slots_embedding, layer_norm
+from .ops import fused_all_slots_embedding, fused_all_slots_embedding_int8, layer_norm, quantize_embedding_int8
 
 
 class RepEncoder(nn.Module):
@@ -25,6 +29,18 @@ class RepEncoder(nn.Module):
         self.slot_num = slot_num
         self.input_norm = nn.LayerNorm(slot_num * emb_dim)
         self.linear = nn.Linear(in_features=slot_num * emb_dim, out_features=d_model)
+        self._int8_weight = None
+        self._int8_scale = None
+
+    def quantize_int8_(self):
+        """Quantise the table to int8 rows + fp32 row scales (online_best/infer.py:980-987)."""
+        with torch.no_grad():
+            self._int8_weight, self._int8_scale = quantize_embedding_int8(self.emb.weight.detach())
+        return self
+
+    def dequantize_(self):
+        self._int8_weight = self._int8_scale = None
+        return self
 
     def flat_inputs(self, batch: dict):
         """(flat_values, val_offsets, flat_row_offsets, batch_size) of a batch.
@@ -51,6 +67,10 @@ class RepEncoder(nn.Module):
         weight = self.emb.weight
         out = torch.empty((batch_size, self.slot_num * self.emb_dim), device=weight.device, dtype=weight.dtype)
         with torch.no_grad():
+            if self._int8_weight is not None:
+                return fused_all_slots_embedding_int8(flat_values, val_offsets, flat_row_offsets, self._int8_weight,
+                                                      self._int8_scale, out, batch_size, self.emb_dim,
+                                                      self.emb.num_embeddings - 1)
             return fused_all_slots_embedding(flat_values, val_offsets, flat_row_offsets, weight.detach(), out,
                                              batch_size, self.emb_dim, self.emb.num_embeddings - 1)
 

@@ -9,6 +9,10 @@ chosen inside), same layout, same results, launched on torch's current stream.
 ``embedding_bag_pooled`` is the general form: per-field tables (possibly of different widths),
 global offsets ``offsets[F*B+1]``, sum or mean pooling, and an explicit output dtype.
 
+``quantize_embedding_int8`` and ``fused_all_slots_embedding_int8`` are the int8 row-quantised
+pair (online_best/infer.py:895-942). A table argument of the general entry points may also be an
+int8 pair ``(q [V, D] int8, scale [V] float32)``; its rows pool as ``acc = fma(q, scale, acc)``.
+
 Both validate their arguments on the host (no device synchronisation) and raise ``ValueError``
 / ``TypeError`` for malformed calls and ``EbagError`` when the C ABI reports a failure.
 """
@@ -36,6 +40,141 @@ def _require_contiguous(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be contiguous")
 
 
+def _split_table(i: int, t):
+    """(rows tensor, scale tensor or None) of one table argument: a tensor or an int8 pair."""
+    if isinstance(t, (tuple, list)):
+        if len(t) != 2:
+            raise ValueError(f"tables[{i}]: an int8 table is a pair (q, scale)")
+        q, scale = t
+        _require_device_tensor(f"tables[{i}][0]", q)
+        _require_device_tensor(f"tables[{i}][1]", scale, q.device)
+        if q.dtype != torch.int8:
+            raise TypeError(f"tables[{i}][0] must be int8 (got {q.dtype})")
+        if scale.dtype != torch.float32 or not scale.is_contiguous() or scale.dim() != 1:
+            raise TypeError(f"tables[{i}][1] must be a contiguous 1-D float32 tensor")
+        if q.dim() == 2 and scale.numel() != q.shape[0]:
+            raise ValueError(f"tables[{i}]: {scale.numel()} scales for {q.shape[0]} rows")
+        return q, scale
+    _require_device_tensor(f"tables[{i}]", t)
+    return t, None
+
+
+def _table_descs(tables):
+    """Validate the table arguments; return (descs, device, dtype code, width, torch dtype)."""
+    num_fields = len(tables)
+    if num_fields == 0:
+        raise ValueError("at least one table is required")
+    parts = [_split_table(i, t) for i, t in enumerate(tables)]
+    dev = parts[0][0].device
+    tdt = parts[0][0].dtype
+    quant = parts[0][1] is not None
+    descs = (_capi.Table * num_fields)()
+    col = 0
+    for i, (t, scale) in enumerate(parts):
+        _require_device_tensor(f"tables[{i}]", t, dev)
+        if (scale is not None) != quant:
+            raise TypeError("tables mix int8 pairs and plain tensors")
+        if t.dim() != 2:
+            raise ValueError(f"tables[{i}] must be 2-D, got shape {tuple(t.shape)}")
+        if t.dtype != tdt:
+            raise TypeError(f"tables[{i}] dtype {t.dtype} differs from tables[0] dtype {tdt}")
+        if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+            raise ValueError(f"tables[{i}] must be row-major with unit column stride")
+        if t.shape[0] < 1:
+            raise ValueError(f"tables[{i}] has no rows")
+        d = descs[i]
+        d.data, d.rows, d.row_stride, d.dim, d.out_col = t.data_ptr(), t.shape[0], t.stride(0), t.shape[1], col
+        d.row_scale = scale.data_ptr() if scale is not None else None
+        col += int(t.shape[1])
+    code = _capi.I8 if quant else _capi.dtype_code(tdt)
+    return descs, dev, code, col, tdt
+
+
+def quantize_embedding_int8(weight: torch.Tensor):
+    """Row-quantise a GPU table to int8: ``(q [V, D] int8, scale [V] float32)``.
+
+    Mirrors online_best/infer.py:895-901 as torch evaluates it on the device:
+    ``scale = max(max_j |w_j| * fp32(1/127), 1e-8)`` (torch turns the division by the Python
+    scalar 127.0 into a multiply by its fp32 reciprocal), ``q = clamp(round_half_even(w / scale),
+    -128, 127)``, all in fp32; bit-identical to that expression for finite tables. ``weight`` is
+    fp32 / bf16 / fp16 with unit column stride.
+    """
+    _require_device_tensor("weight", weight)
+    if weight.dim() != 2 or weight.stride(1) != 1 or weight.stride(0) < weight.shape[1]:
+        raise ValueError("weight must be a row-major 2-D tensor with unit column stride")
+    rows, dim = weight.shape
+    dev = weight.device
+    q = torch.empty((rows, dim), dtype=torch.int8, device=dev)
+    scale = torch.empty(rows, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _capi.check(_capi.lib().cti_ebag_quantize_int8(
+            weight.data_ptr(), _capi.dtype_code(weight.dtype), rows, dim, weight.stride(0), q.data_ptr(),
+            scale.data_ptr(), _capi.current_stream_handle(dev)))
+    return q, scale
+
+
+def _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev):
+    for name, t in (("flat_values", flat_values), ("val_offsets", val_offsets),
+                    ("flat_row_offsets", flat_row_offsets), ("out", out)):
+        _require_device_tensor(name, t, dev)
+        _require_contiguous(name, t)
+    for name, t in (("flat_values", flat_values), ("val_offsets", val_offsets),
+                    ("flat_row_offsets", flat_row_offsets)):
+        if t.dtype != torch.int64:
+            raise TypeError(f"{name} must be int64 (got {t.dtype})")
+
+
+def fused_all_slots_embedding_int8(
+    flat_values: torch.Tensor,
+    val_offsets: torch.Tensor,
+    flat_row_offsets: torch.Tensor,
+    weight_int8: torch.Tensor,
+    scale: torch.Tensor,
+    out: torch.Tensor,
+    batch_size: int,
+    emb_dim: int,
+    max_idx: int,
+) -> torch.Tensor:
+    """int8 drop-in for ``fused_all_slots_embedding_kernel_int8[(B, S)](values, val_offsets,
+    row_offsets, weight_int8, scale, out, batch_size, emb_dim, max_idx, BLOCK_SIZE)``
+    (online_best/infer.py:904-942, launched at online_best/infer.py:991-996).
+
+    ``weight_int8`` int8 [V, emb_dim] and ``scale`` float32 [V] as made by
+    ``quantize_embedding_int8``; each bag accumulates ``fma(q, scale[row], acc)`` in fp32 in
+    element order; ``out`` [B, S*emb_dim] is written in its own dtype (fp32 / bf16 / fp16; the
+    reference stores bf16, :940). Returns ``out``.
+    """
+    dev = weight_int8.device
+    _require_device_tensor("weight_int8", weight_int8)
+    _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
+    _require_device_tensor("scale", scale, dev)
+    _require_contiguous("weight_int8", weight_int8)
+    _require_contiguous("scale", scale)
+    if weight_int8.dtype != torch.int8 or weight_int8.dim() != 2:
+        raise TypeError(f"weight_int8 must be a 2-D int8 tensor (got {weight_int8.dtype}, {weight_int8.dim()}-D)")
+    if scale.dtype != torch.float32 or scale.numel() != weight_int8.shape[0]:
+        raise TypeError(f"scale must be float32 with {weight_int8.shape[0]} elements")
+    batch_size, emb_dim, max_idx = int(batch_size), int(emb_dim), int(max_idx)
+    num_slots = val_offsets.numel()
+    if weight_int8.shape[1] != emb_dim:
+        raise ValueError(f"weight_int8 has {weight_int8.shape[1]} columns, emb_dim is {emb_dim}")
+    if not 0 <= max_idx < weight_int8.shape[0]:
+        raise ValueError(f"max_idx {max_idx} outside [0, {weight_int8.shape[0] - 1}]")
+    if batch_size < 0:
+        raise ValueError(f"batch_size must be >= 0, got {batch_size}")
+    if flat_row_offsets.numel() != num_slots * (batch_size + 1):
+        raise ValueError(f"flat_row_offsets has {flat_row_offsets.numel()} entries, expected "
+                         f"{num_slots} * ({batch_size} + 1)")
+    if out.numel() != batch_size * num_slots * emb_dim or (out.dim() >= 1 and out.shape[0] != batch_size):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected ({batch_size}, {num_slots * emb_dim})")
+    with torch.cuda.device(dev):
+        _capi.check(_capi.lib().cti_ebag_fused_all_slots_int8(
+            flat_values.data_ptr(), val_offsets.data_ptr(), flat_row_offsets.data_ptr(), weight_int8.data_ptr(),
+            scale.data_ptr(), out.data_ptr(), _capi.dtype_code(out.dtype), batch_size, num_slots, emb_dim, max_idx,
+            flat_values.numel(), _capi.current_stream_handle(dev)))
+    return out
+
+
 def fused_all_slots_embedding(
     flat_values: torch.Tensor,
     val_offsets: torch.Tensor,
@@ -61,14 +200,7 @@ def fused_all_slots_embedding(
     """
     dev = weight.device
     _require_device_tensor("weight", weight)
-    for name, t in (("flat_values", flat_values), ("val_offsets", val_offsets),
-                    ("flat_row_offsets", flat_row_offsets), ("out", out)):
-        _require_device_tensor(name, t, dev)
-        _require_contiguous(name, t)
-    for name, t in (("flat_values", flat_values), ("val_offsets", val_offsets),
-                    ("flat_row_offsets", flat_row_offsets)):
-        if t.dtype != torch.int64:
-            raise TypeError(f"{name} must be int64 (got {t.dtype})")
+    _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
     if weight.dim() != 2:
         raise ValueError(f"weight must be 2-D [V, D], got shape {tuple(weight.shape)}")
     _require_contiguous("weight", weight)
@@ -122,7 +254,7 @@ def fused_embedding(batch: dict, weight: torch.Tensor, slot_num: int, out: Optio
 def embedding_bag_pooled(
     values: torch.Tensor,
     offsets: torch.Tensor,
-    tables: Sequence[torch.Tensor],
+    tables: Sequence,
     pooling: str = "sum",
     out_dtype: Optional[torch.dtype] = None,
     out: Optional[torch.Tensor] = None,
@@ -136,8 +268,10 @@ def embedding_bag_pooled(
       offsets  int64 [F*B+1]; bag (f, b) = values[offsets[f*B+b] : offsets[f*B+b+1]]
       tables   F row-major 2-D tensors [V_f, D_f] of one dtype (fp32 / bf16 / fp16); row
                stride may exceed D_f. Field f fills columns [sum_{g<f} D_g, ... + D_f).
+               Or F int8 pairs (q [V_f, D_f] int8, scale [V_f] float32): element =
+               q * scale[row], fused into the accumulation (one fma per element).
       pooling  'sum' or 'mean' (mean of an empty bag is 0)
-      out_dtype defaults to the tables' dtype; ``out`` (if given) must be contiguous
+      out_dtype defaults to the tables' dtype (bfloat16 for int8 tables); ``out`` (if given) must be contiguous
                [B, sum(D_f)] of that dtype.
       long_threshold  bags longer than this are split over the lane groups of a wavefront
                (0 = per-shape default, -1 = split every non-empty bag).
@@ -149,20 +283,7 @@ def embedding_bag_pooled(
     mode=pooling) followed by concatenation along dim 1 (baseline/infer.py:256-263).
     """
     num_fields = len(tables)
-    if num_fields == 0:
-        raise ValueError("at least one table is required")
-    dev = tables[0].device
-    tdt = tables[0].dtype
-    for i, t in enumerate(tables):
-        _require_device_tensor(f"tables[{i}]", t, dev)
-        if t.dim() != 2:
-            raise ValueError(f"tables[{i}] must be 2-D, got shape {tuple(t.shape)}")
-        if t.dtype != tdt:
-            raise TypeError(f"tables[{i}] dtype {t.dtype} differs from tables[0] dtype {tdt}")
-        if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
-            raise ValueError(f"tables[{i}] must be row-major with unit column stride")
-        if t.shape[0] < 1:
-            raise ValueError(f"tables[{i}] has no rows")
+    descs, dev, tcode, width, tdt = _table_descs(tables)
     _require_device_tensor("values", values, dev)
     _require_device_tensor("offsets", offsets, dev)
     _require_contiguous("values", values)
@@ -172,9 +293,7 @@ def embedding_bag_pooled(
     if (offsets.numel() - 1) % num_fields != 0 or offsets.numel() < 1:
         raise ValueError(f"offsets has {offsets.numel()} entries; expected F*B+1 with F={num_fields}")
     batch_size = (offsets.numel() - 1) // num_fields
-    dims = [int(t.shape[1]) for t in tables]
-    width = sum(dims)
-    odt = tdt if out_dtype is None else out_dtype
+    odt = _default_out_dtype(tdt) if out_dtype is None else out_dtype
     if out is None:
         out = torch.empty((batch_size, width), device=dev, dtype=odt)
     else:
@@ -184,15 +303,6 @@ def embedding_bag_pooled(
             raise TypeError(f"out dtype {out.dtype} differs from requested {odt}")
         if tuple(out.shape) != (batch_size, width):
             raise ValueError(f"out has shape {tuple(out.shape)}, expected ({batch_size}, {width})")
-    descs = (_capi.Table * num_fields)()
-    col = 0
-    for i, t in enumerate(tables):
-        descs[i].data = t.data_ptr()
-        descs[i].rows = t.shape[0]
-        descs[i].row_stride = t.stride(0)
-        descs[i].dim = dims[i]
-        descs[i].out_col = col
-        col += dims[i]
     opts = _capi.Options()
     opts.long_threshold = int(long_threshold)
     opts.use_bins = int(bool(use_bins))
@@ -206,10 +316,15 @@ def embedding_bag_pooled(
         stream = _capi.current_stream_handle(dev)
         _capi.check(lib.cti_ebag_forward(
             values.data_ptr(), _capi.index_code(values.dtype), values.numel(), offsets.data_ptr(),
-            batch_size, num_fields, descs, _capi.dtype_code(tdt), _capi.pooling_code(pooling),
+            batch_size, num_fields, descs, tcode, _capi.pooling_code(pooling),
             out.data_ptr(), _capi.dtype_code(odt), width, ws.data_ptr() if ws is not None else None, ws_bytes,
             ctypes.byref(opts), stream))
     return out
+
+
+def _default_out_dtype(tdt: torch.dtype) -> torch.dtype:
+    """Output dtype when none is given: the tables' dtype, bfloat16 for int8 tables (:940)."""
+    return torch.bfloat16 if tdt == torch.int8 else tdt
 
 
 class PooledEmbedding:
@@ -221,31 +336,16 @@ class PooledEmbedding:
     counter every call leaves at zero (calls on one plan must not overlap).
     """
 
-    def __init__(self, tables: Sequence[torch.Tensor], pooling: str = "sum",
+    def __init__(self, tables: Sequence, pooling: str = "sum",
                  out_dtype: Optional[torch.dtype] = None, long_threshold: int = 0,
                  use_bins: bool = False, block_threshold: int = 0, max_batch: int = 0):
-        if len(tables) == 0:
-            raise ValueError("at least one table is required")
-        self.tables = list(tables)
-        self.device = self.tables[0].device
-        tdt = self.tables[0].dtype
-        for i, t in enumerate(self.tables):
-            _require_device_tensor(f"tables[{i}]", t, self.device)
-            if t.dim() != 2 or t.dtype != tdt or t.stride(1) != 1 or t.stride(0) < t.shape[1] or t.shape[0] < 1:
-                raise ValueError(f"tables[{i}] must be a non-empty row-major 2-D tensor of dtype {tdt}")
+        self.tables = list(tables)  # keeps the tensors (and int8 scales) alive
+        self._descs, self.device, self._tdt, self.width, tdt = _table_descs(self.tables)
         self.num_fields = len(self.tables)
-        self.width = sum(int(t.shape[1]) for t in self.tables)
         self.table_dtype = tdt
-        self.out_dtype = tdt if out_dtype is None else out_dtype
-        self._tdt = _capi.dtype_code(tdt)
+        self.out_dtype = _default_out_dtype(tdt) if out_dtype is None else out_dtype
         self._odt = _capi.dtype_code(self.out_dtype)
         self._pool = _capi.pooling_code(pooling)
-        self._descs = (_capi.Table * self.num_fields)()
-        col = 0
-        for i, t in enumerate(self.tables):
-            d = self._descs[i]
-            d.data, d.rows, d.row_stride, d.dim, d.out_col = t.data_ptr(), t.shape[0], t.stride(0), t.shape[1], col
-            col += int(t.shape[1])
         self._opts = _capi.Options()
         self._opts.long_threshold = int(long_threshold)
         self._opts.use_bins = int(bool(use_bins))

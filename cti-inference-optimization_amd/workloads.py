@@ -62,23 +62,26 @@ class Workload:
     def lengths(self) -> np.ndarray:
         return np.diff(self.offsets)
 
-    def bytes_algorithmic(self) -> int:
-        """Each lookup's row once, plus indices, offsets and the output (logical bytes)."""
-        tb = torch.tensor([], dtype=self.table_dtype).element_size()
+    def bytes_algorithmic(self, int8: bool = False) -> int:
+        """Each lookup's row once, plus indices, offsets and the output (logical bytes).
+        With ``int8`` the rows are int8 row-quantised: 1 byte per element + a 4-byte scale."""
+        tb = 1 if int8 else torch.tensor([], dtype=self.table_dtype).element_size()
+        extra = 4 if int8 else 0
         ob = torch.tensor([], dtype=self.out_dtype).element_size()
         L = self.lengths().reshape(self.num_fields, self.batch).sum(axis=1)
-        rows = int(sum(int(L[f]) * self.dims[f] * tb for f in range(self.num_fields)))
+        rows = int(sum(int(L[f]) * (self.dims[f] * tb + extra) for f in range(self.num_fields)))
         return rows + self.nnz * self.values.itemsize + self.offsets.size * 8 + self.batch * sum(self.dims) * ob
 
-    def bytes_compulsory(self) -> int:
+    def bytes_compulsory(self, int8: bool = False) -> int:
         """As bytes_algorithmic, but each distinct (field, row) read once."""
-        tb = torch.tensor([], dtype=self.table_dtype).element_size()
+        tb = 1 if int8 else torch.tensor([], dtype=self.table_dtype).element_size()
+        extra = 4 if int8 else 0
         ob = torch.tensor([], dtype=self.out_dtype).element_size()
         total = 0
         for f in range(self.num_fields):
             s, e = int(self.offsets[f * self.batch]), int(self.offsets[(f + 1) * self.batch])
             rows = np.clip(self.values[s:e], 0, self.vocab[f] - 1)
-            total += np.unique(rows).size * self.dims[f] * tb
+            total += np.unique(rows).size * (self.dims[f] * tb + extra)
         return total + self.nnz * self.values.itemsize + self.offsets.size * 8 + self.batch * sum(self.dims) * ob
 
 

@@ -41,12 +41,14 @@
 extern "C" {
 #endif
 
-#define CTI_EBAG_ABI_VERSION 1
+#define CTI_EBAG_ABI_VERSION 2
 
 /* element types of tables and outputs */
 #define CTI_EBAG_F32 0
 #define CTI_EBAG_BF16 1
 #define CTI_EBAG_F16 2
+/* int8 row-quantised tables only (online_best/infer.py:893-942): element = q * row_scale[row] */
+#define CTI_EBAG_I8 3
 
 /* index (sign id) types */
 #define CTI_EBAG_I64 0
@@ -65,13 +67,15 @@ extern "C" {
 
 /* One field's table. `data` is a device pointer to a row-major [rows, row_stride] matrix of
  * which the first `dim` columns are used. `out_col` is the first output column of the field.
- * Several fields may share one `data` pointer (the reference's single shared nn.Embedding). */
+ * Several fields may share one `data` pointer (the reference's single shared nn.Embedding).
+ * `row_scale` (fp32 [rows], device) is required for CTI_EBAG_I8 tables and ignored otherwise. */
 typedef struct cti_ebag_table {
   const void* data;
   int64_t rows;
   int64_t row_stride; /* elements between consecutive rows, >= dim */
   int32_t dim;
   int32_t out_col;
+  const float* row_scale;
 } cti_ebag_table;
 
 /* Tuning knobs of one call. Zero-initialise and set only what you need:
@@ -121,7 +125,8 @@ int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* val_offsets,
  *   values        [nnz] sign ids of type `index_type`, field-major
  *   offsets       int64 [num_fields*B + 1]; bag (f, b) = values[offsets[f*B+b] : offsets[f*B+b+1]]
  *   tables        host array of num_fields descriptors (read during the call only)
- *   table_dtype   element type shared by all tables
+ *   table_dtype   element type shared by all tables (CTI_EBAG_I8: int8 rows times each table's
+ *                 row_scale, pooled as acc = fma(q, scale, acc))
  *   pooling       CTI_EBAG_SUM or CTI_EBAG_MEAN (mean of an empty bag is 0)
  *   out           [B, out_row_stride] of `out_dtype`; field f writes columns
  *                 [out_col_f, out_col_f + dim_f)
@@ -176,6 +181,31 @@ int cti_ebag_merge_batches(const int64_t* const* sub_values,
                            const int64_t* sub_nnz, int32_t num_sub, int32_t num_slots,
                            int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
                            int64_t* global_offsets, void* stream);
+
+/*
+ * int8 variant of the reference-layout entry point, a drop-in for the launch
+ *   fused_all_slots_embedding_kernel_int8[(batch_size, num_slots)](values, val_offsets,
+ *       row_offsets, weight_int8, scale, out, batch_size, emb_dim, max_idx, BLOCK_SIZE)
+ * (online_best/infer.py:904-942, launched at :991-996): as cti_ebag_fused_all_slots, with
+ *   weight_int8  int8 [max_idx+1, emb_dim]  and  scale  fp32 [max_idx+1];
+ *   acc = fma(q, scale[row], acc) per element in element order, out written in `out_dtype`
+ *   (the reference writes bf16, :940).
+ */
+int cti_ebag_fused_all_slots_int8(const int64_t* values, const int64_t* val_offsets,
+                                  const int64_t* row_offsets, const int8_t* weight_int8,
+                                  const float* scale, void* out, int32_t out_dtype, int64_t batch_size,
+                                  int32_t num_slots, int32_t emb_dim, int64_t max_idx, int64_t nnz,
+                                  void* stream);
+
+/*
+ * Row quantisation of a table to int8, as quantize_embedding_int8 (online_best/infer.py:895-901):
+ *   m = max_j |w[r, j]| (fp32), s = max(m / 127, 1e-8) (fp32), q[r, j] = clamp(rint(w / s), -128, 127)
+ * with fp32 IEEE division and round half to even, bit for bit.
+ *   weight  [rows, row_stride] of `dtype` (F32/BF16/F16), first `dim` columns used
+ *   q       int8 [rows, dim] (contiguous), scale fp32 [rows]. Tables must be finite.
+ */
+int cti_ebag_quantize_int8(const void* weight, int32_t dtype, int64_t rows, int64_t dim, int64_t row_stride,
+                           int8_t* q, float* scale, void* stream);
 
 /*
  * Row LayerNorm over the pooled block, a drop-in for the launch

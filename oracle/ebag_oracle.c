@@ -16,9 +16,17 @@
  * bag -> 0). Accumulation is strictly sequential in element order, as in the reference kernel's
  * loop, so a bag pooled by one lane group on the GPU matches this bit for bit.
  *
+ *   - online_best/infer.py:904-942  fused_all_slots_embedding_kernel_int8: the same loop over an
+ *     int8 table with one fp32 scale per row, acc += int8_row * scale_val (:934-936). Triton
+ *     fuses that multiply-add (its default fp-fusion), so the restatement is acc = fmaf(q, s, acc)
+ *     in element order, with C99 fmaf (exact product and sum, one rounding).
+ *   - online_best/infer.py:895-901  quantize_embedding_int8 as evaluated by torch on the device:
+ *     s = max(max_j |w_j| * RN32(1/127), 1e-8) (a Python-scalar divisor becomes a multiply by its
+ *     fp32 reciprocal), q_j = clamp(round_half_even(w_j / s), -128, 127) with IEEE fp32 division.
+ *
  * Conversions are written from the IEEE 754 definitions: bf16 = high half of the fp32 word,
  * fp32 -> bf16/fp16 round to nearest, ties to even; NaN stays NaN.
- * Build with -ffp-contract=off (no fused multiply-add anywhere).
+ * Build with -ffp-contract=off (no fused multiply-add anywhere except the explicit fmaf).
  */
 #include <math.h>
 #include <stdint.h>
@@ -27,6 +35,7 @@
 #define OR_F32 0
 #define OR_BF16 1
 #define OR_F16 2
+#define OR_I8 3 /* int8 table rows times the table's per-row fp32 scale */
 
 typedef struct oracle_table {
   const void* data;
@@ -34,6 +43,7 @@ typedef struct oracle_table {
   int64_t row_stride; /* elements */
   int32_t dim;
   int32_t out_col;
+  const float* row_scale; /* OR_I8 tables: fp32 [rows] */
 } oracle_table;
 
 static float u32_as_f32(uint32_t u) {
@@ -142,7 +152,13 @@ int oracle_pool(const void* values, int32_t idx32, int64_t nnz, const int64_t* o
           int64_t v = idx32 ? (int64_t)((const int32_t*)values)[i] : ((const int64_t*)values)[i];
           int64_t r = clamp64(v, 0, t->rows - 1);
           const int64_t row0 = r * t->row_stride + c0;
-          for (int32_t c = 0; c < nc; ++c) acc[c] = acc[c] + load_elem(t->data, tdt, row0 + c);
+          if (tdt == OR_I8) {
+            const int8_t* q = (const int8_t*)t->data + row0;
+            const float sc = t->row_scale[r];
+            for (int32_t c = 0; c < nc; ++c) acc[c] = fmaf((float)q[c], sc, acc[c]);
+          } else {
+            for (int32_t c = 0; c < nc; ++c) acc[c] = acc[c] + load_elem(t->data, tdt, row0 + c);
+          }
         }
         const int64_t L = end - start;
         for (int32_t c = 0; c < nc; ++c) {
@@ -154,6 +170,39 @@ int oracle_pool(const void* values, int32_t idx32, int64_t nnz, const int64_t* o
     }
   }
   return 0;
+}
+
+/*
+ * Row quantisation (online_best/infer.py:895-901) of a [rows, row_stride] table of type dt
+ * (first dim columns used) into q int8 [rows, dim] and scale fp32 [rows]. Finite inputs.
+ */
+int oracle_quantize_int8(const void* w, int32_t dt, int64_t rows, int64_t dim, int64_t row_stride, int8_t* q,
+                         float* scale) {
+  if (rows < 0 || dim < 1 || row_stride < dim || dt < OR_F32 || dt > OR_F16) return -1;
+  for (int64_t r = 0; r < rows; ++r) {
+    float m = 0.0f;
+    for (int64_t c = 0; c < dim; ++c) {
+      const float a = fabsf(load_elem(w, dt, r * row_stride + c));
+      if (a > m) m = a;
+    }
+    /* row_max / 127.0 with a Python-scalar divisor: torch's device kernel multiplies by the fp32
+     * reciprocal of the scalar (ATen's div_true_kernel_cuda, "a * reciprocal(b)") */
+    float s = m * (1.0f / 127.0f);
+    if (s < 1e-8f) s = 1e-8f;
+    scale[r] = s;
+    for (int64_t c = 0; c < dim; ++c) {
+      float v = nearbyintf(load_elem(w, dt, r * row_stride + c) / s); /* default mode: ties to even */
+      if (v < -128.0f) v = -128.0f;
+      if (v > 127.0f) v = 127.0f;
+      q[r * dim + c] = (int8_t)v;
+    }
+  }
+  return 0;
+}
+
+/* fmaf over arrays, exposed so the tests can pin the C library's fused multiply-add. */
+void oracle_fmaf_array(const float* a, const float* b, const float* c, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = fmaf(a[i], b[i], c[i]);
 }
 
 /* Elementwise conversions exposed for the tests that pin them against library routines. */

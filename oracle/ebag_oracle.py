@@ -12,9 +12,13 @@ CPU restatements of the fused sparse-feature embedding-bag path:
   merge_layouts      online_best/infer.py:581-631 (per-slot concatenation of sub-batches)
   merge_pair_layouts online_best/infer.py:2977-3037 (same, with its int32 round trip)
   layer_norm_np      online_best/infer.py:829-858 (row LayerNorm of the pooled block, fp32)
+  quantize_int8_np / quantize_int8_c   online_best/infer.py:895-901 (int8 rows + fp32 scales)
+  fma_np             fp32 fused multiply-add emulated exactly in float64 (round to odd)
   bf16 / fp16 encoders and decoders (IEEE round to nearest even)
 
-Table arrays: float32 arrays for 'f32'; uint16 bit patterns for 'bf16' and 'f16'.
+Table arrays: float32 arrays for 'f32'; uint16 bit patterns for 'bf16' and 'f16'; for 'i8' a
+pair (int8 [rows, dim], float32 scale [rows]) pooled as acc = fma(q, scale[row], acc)
+(online_best/infer.py:904-942).
 Pooling semantics (online_best/infer.py:805-827, baseline/infer.py:256-263): row index
 clamp(v, 0, rows-1); fp32 accumulator starting at +0, rows added in element order; mean divides
 the fp32 sum by the bag length; empty bag -> 0; one rounding to the output type.
@@ -31,7 +35,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle_ebag.so")
 
-DTYPES = {"f32": 0, "bf16": 1, "f16": 2}
+DTYPES = {"f32": 0, "bf16": 1, "f16": 2, "i8": 3}
 
 
 # ------------------------------------------------------------------------------------------------
@@ -92,6 +96,52 @@ def _bag_bounds(offsets, val_base, stride, f, batch, nnz):
     return s, e
 
 
+def _rows_of(tab):
+    """The row array of a table ('i8' tables are (q, scale) pairs)."""
+    return tab[0] if isinstance(tab, tuple) else tab
+
+
+def fma_np(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """fp32 fma(a, b, c) = RN32(a*b + c) with one rounding, for finite inputs.
+
+    a*b is exact in float64 (24 + 24 bits). The sum a*b + c is formed in float64 rounded to odd
+    (TwoSum gives the rounding error; a non-zero error with an even last bit moves the sum one
+    float64 step towards the exact value), and rounding that to fp32 is the correctly rounded
+    result since 53 >= 24 + 2 (Boldo & Melquiond, "Emulation of FMA and correctly rounded sums:
+    proved algorithms using rounding to odd", IEEE Trans. Computers 57(4), 2008).
+    """
+    a64 = np.asarray(a, np.float32).astype(np.float64)
+    b64 = np.asarray(b, np.float32).astype(np.float64)
+    c64 = np.asarray(c, np.float32).astype(np.float64)
+    p = a64 * b64
+    p, c64 = np.broadcast_arrays(p, c64)
+    ssum = p + c64
+    bb = ssum - p
+    err = (p - (ssum - bb)) + (c64 - bb)
+    even = (ssum.view(np.uint64) & np.uint64(1)) == 0
+    bump = (err != 0) & even
+    towards = np.where(err > 0, np.inf, -np.inf)
+    ro = np.where(bump, np.nextafter(ssum, towards), ssum)
+    return ro.astype(np.float32)
+
+
+def quantize_int8_np(w: np.ndarray):
+    """online_best/infer.py:895-901 as torch evaluates it on the device, in fp32.
+
+    w: float32 [rows, dim] (decoded table). row_max = max |w| (:897); scale = row_max / 127.0,
+    which torch's device kernel computes as row_max * RN32(1/127) (a Python-scalar divisor is
+    turned into a multiply by its fp32 reciprocal) (:898); clamp(min=1e-8) (:899);
+    q = round_half_even(w / scale), IEEE fp32 division, clamp to [-128, 127], int8 (:900).
+    Returns (q int8 [rows, dim], scale float32 [rows]).
+    """
+    w = np.asarray(w, np.float32)
+    m = np.abs(w).max(axis=1) if w.shape[1] else np.zeros(w.shape[0], np.float32)
+    inv127 = np.float32(1.0) / np.float32(127.0)
+    scale = np.maximum((m * inv127).astype(np.float32), np.float32(1e-8)).astype(np.float32)
+    q = np.clip(np.rint((w / scale[:, None]).astype(np.float32)), -128, 127).astype(np.int8)
+    return q, scale
+
+
 def pool_np(values: np.ndarray, offsets: np.ndarray, tables: Sequence[np.ndarray], table_dtype: str,
             pooling: str = "sum", out_dtype: Optional[str] = None, batch: Optional[int] = None,
             val_base: Optional[np.ndarray] = None, out_cols: Optional[Sequence[int]] = None,
@@ -110,12 +160,12 @@ def pool_np(values: np.ndarray, offsets: np.ndarray, tables: Sequence[np.ndarray
         stride = batch
     else:
         stride = batch + 1
-    dims = [t.shape[1] for t in tables]
+    dims = [_rows_of(t).shape[1] for t in tables]
     cols = list(np.cumsum([0] + dims[:-1])) if out_cols is None else list(out_cols)
     width = sum(dims) if out_width is None else out_width
     out = np.zeros((batch, width), dtype=np.float32)
     for f, tab in enumerate(tables):
-        rows_f = tab.shape[0]
+        rows_f = _rows_of(tab).shape[0]
         s, e = _bag_bounds(offsets, val_base, stride, f, batch, nnz)
         L = e - s
         acc = np.zeros((batch, dims[f]), dtype=np.float32)
@@ -123,7 +173,11 @@ def pool_np(values: np.ndarray, offsets: np.ndarray, tables: Sequence[np.ndarray
         for k in range(maxL):
             m = L > k
             rows = np.clip(values[s[m] + k], 0, rows_f - 1)
-            acc[m] = acc[m] + decode(tab[rows], table_dtype)
+            if table_dtype == "i8":
+                q, sc = tab
+                acc[m] = fma_np(q[rows].astype(np.float32), np.asarray(sc, np.float32)[rows][:, None], acc[m])
+            else:
+                acc[m] = acc[m] + decode(tab[rows], table_dtype)
         if pooling == "mean":
             nz = L > 0
             acc[nz] = acc[nz] / L[nz].astype(np.float32)[:, None]
@@ -136,7 +190,7 @@ def pool_np(values: np.ndarray, offsets: np.ndarray, tables: Sequence[np.ndarray
 # ------------------------------------------------------------------------------------------------
 class _Table(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("rows", ctypes.c_int64), ("row_stride", ctypes.c_int64),
-                ("dim", ctypes.c_int32), ("out_col", ctypes.c_int32)]
+                ("dim", ctypes.c_int32), ("out_col", ctypes.c_int32), ("row_scale", ctypes.c_void_p)]
 
 
 _clib = None
@@ -163,6 +217,11 @@ def clib() -> ctypes.CDLL:
         for n in ("oracle_f32_to_bf16_array", "oracle_f32_to_f16_array", "oracle_f16_to_f32_array"):
             getattr(lib, n).restype = None
             getattr(lib, n).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        lib.oracle_quantize_int8.restype = ctypes.c_int
+        lib.oracle_quantize_int8.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64,
+                                             ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+        lib.oracle_fmaf_array.restype = None
+        lib.oracle_fmaf_array.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64]
         lib.oracle_num_threads.restype = ctypes.c_int
         lib.oracle_set_num_threads.argtypes = [ctypes.c_int]
         _clib = lib
@@ -192,13 +251,19 @@ def pool_c(values: np.ndarray, offsets: np.ndarray, tables: Sequence[np.ndarray]
     else:
         stride = batch + 1
         vb = np.ascontiguousarray(val_base, dtype=np.int64)
-    dims = [t.shape[1] for t in tables]
+    dims = [_rows_of(t).shape[1] for t in tables]
     cols = list(np.cumsum([0] + dims[:-1])) if out_cols is None else list(out_cols)
     width = sum(dims) if out_width is None else out_width
     descs = (_Table * F)()
     keep = []
     for f, t in enumerate(tables):
-        t = np.ascontiguousarray(t)
+        if table_dtype == "i8":
+            sc = np.ascontiguousarray(t[1], dtype=np.float32)
+            t = np.ascontiguousarray(t[0], dtype=np.int8)
+            keep.append(sc)
+            descs[f].row_scale = sc.ctypes.data
+        else:
+            t = np.ascontiguousarray(t)
         keep.append(t)
         descs[f].data = t.ctypes.data
         descs[f].rows = t.shape[0] if table_rows is None else int(table_rows[f])
@@ -216,6 +281,28 @@ def pool_c(values: np.ndarray, offsets: np.ndarray, tables: Sequence[np.ndarray]
 
 
 pool = pool_c
+
+
+def quantize_int8_c(table: np.ndarray, table_dtype: str = "f32"):
+    """The C restatement of quantize_int8_np; ``table`` in the encoding of ``table_dtype``."""
+    table = np.ascontiguousarray(table)
+    rows, dim = table.shape
+    q = np.empty((rows, dim), dtype=np.int8)
+    scale = np.empty(rows, dtype=np.float32)
+    rc = clib().oracle_quantize_int8(table.ctypes.data, DTYPES[table_dtype], rows, dim, dim, q.ctypes.data,
+                                     scale.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle_quantize_int8 rejected its arguments")
+    return q, scale
+
+
+def c_fmaf(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """C99 fmaf elementwise (the operation the C oracle pools int8 tables with)."""
+    a, b, c = (np.ascontiguousarray(np.broadcast_to(x, np.broadcast_shapes(np.shape(a), np.shape(b), np.shape(c))),
+                                    dtype=np.float32) for x in (a, b, c))
+    y = np.empty(a.shape, dtype=np.float32)
+    clib().oracle_fmaf_array(a.ctypes.data, b.ctypes.data, c.ctypes.data, y.ctypes.data, a.size)
+    return y
 
 
 def c_f32_to_bf16(x: np.ndarray) -> np.ndarray:

@@ -20,7 +20,8 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     names = declared_functions()
     for n in ("cti_ebag_fused_all_slots", "cti_ebag_forward", "cti_ebag_pack_slots", "cti_ebag_merge_batches",
-              "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version"):
+              "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version", "cti_ebag_layernorm",
+              "cti_ebag_fused_all_slots_int8", "cti_ebag_quantize_int8"):
         assert n in names
 
 
@@ -40,8 +41,8 @@ def test_status_codes_match_header(pkg):
     for name in ("OK", "EINVAL", "EUNSUPPORTED", "EHIP", "EWORKSPACE"):
         v = int(re.search(rf"#define CTI_EBAG_{name} \(?(-?\d+)\)?", text).group(1))
         assert getattr(pkg._capi, name) == v
-    for name, attr in (("F32", "F32"), ("BF16", "BF16"), ("F16", "F16"), ("I64", "I64"), ("I32", "I32"),
-                       ("SUM", "SUM"), ("MEAN", "MEAN")):
+    for name, attr in (("F32", "F32"), ("BF16", "BF16"), ("F16", "F16"), ("I8", "I8"), ("I64", "I64"),
+                       ("I32", "I32"), ("SUM", "SUM"), ("MEAN", "MEAN")):
         v = int(re.search(rf"#define CTI_EBAG_{name} (\d+)", text).group(1))
         assert getattr(pkg._capi, attr) == v
 
@@ -64,7 +65,18 @@ def _table(pkg, **kw):
     t[0].row_stride = kw.get("row_stride", 128)
     t[0].dim = kw.get("dim", 128)
     t[0].out_col = kw.get("out_col", 0)
+    t[0].row_scale = kw.get("row_scale", None)
     return t
+
+
+def test_table_struct_matches_header(pkg):
+    """Field order and size of cti_ebag_table as the header declares it."""
+    text = open(HEADER).read()
+    body = re.search(r"typedef struct cti_ebag_table \{(.*?)\} cti_ebag_table;", text, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = re.findall(r"(\w+)\s*;", body)
+    assert fields == [f[0] for f in pkg._capi.Table._fields_]
+    assert ctypes.sizeof(pkg._capi.Table) == 40
 
 
 @pytest.mark.parametrize("kw,needle", [
@@ -170,3 +182,47 @@ def test_python_wrappers_validate_before_any_launch(pkg):
         pkg._capi.dtype_code(torch.int8)
     with pytest.raises(ValueError):
         pkg._capi.pooling_code("max")
+
+
+def test_int8_tables_need_scales(pkg):
+    c = pkg._capi
+    rc = _forward(pkg, tables=_table(pkg, data=256), tdt=c.I8)
+    assert rc == c.EINVAL and "row_scale" in c.last_error()
+
+
+def test_fused_all_slots_int8_rejects_bad_arguments(pkg):
+    c = pkg._capi
+    f = c.lib().cti_ebag_fused_all_slots_int8
+    #      values val_off row_off weight scale out odt     B  S   D    max_idx nnz stream
+    assert f(256, 256, 256, 256, None, 256, c.BF16, 4, 28, 128, 10, 5, None) == c.EINVAL
+    assert "scale" in c.last_error()
+    assert f(256, 256, 256, 256, 256, 256, c.I8, 4, 28, 128, 10, 5, None) == c.EINVAL
+    assert "output dtype" in c.last_error()
+    assert f(256, 256, 256, 256, 256, 256, c.BF16, 4, 28, 0, 10, 5, None) == c.EINVAL
+    assert f(256, 256, 256, 256, 256, 256, c.BF16, 4, 28, 128, 2 ** 31, 5, None) == c.EUNSUPPORTED
+    assert f(None, None, None, None, None, None, c.BF16, 0, 28, 128, 10, 0, None) == c.OK
+    # the float entry point does not take the int8 code
+    assert c.lib().cti_ebag_fused_all_slots(256, 256, 256, 256, c.I8, 256, 4, 28, 128, 10, 5, None) == c.EINVAL
+
+
+def test_quantize_int8_rejects_bad_arguments(pkg):
+    c = pkg._capi
+    f = c.lib().cti_ebag_quantize_int8
+    #      weight dtype  rows dim stride q   scale stream
+    assert f(256, c.I8, 10, 128, 128, 256, 256, None) == c.EINVAL
+    assert f(256, c.BF16, -1, 128, 128, 256, 256, None) == c.EINVAL
+    assert f(256, c.BF16, 10, 0, 0, 256, 256, None) == c.EINVAL
+    assert f(256, c.BF16, 10, 128, 64, 256, 256, None) == c.EINVAL and "row_stride" in c.last_error()
+    assert f(256, c.BF16, 10, 128, 128, None, 256, None) == c.EINVAL
+    assert f(None, c.BF16, 0, 128, 128, None, None, None) == c.OK
+
+
+def test_int8_python_wrappers_validate_before_any_launch(pkg):
+    q = torch.zeros(10, 16, dtype=torch.int8)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        pkg.quantize_embedding_int8(torch.zeros(10, 16))
+    with pytest.raises(ValueError, match="GPU tensor"):
+        pkg.embedding_bag_pooled(torch.zeros(3, dtype=torch.int64), torch.zeros(5, dtype=torch.int64),
+                                 [(q, torch.ones(10))])
+    with pytest.raises(ValueError, match="pair"):
+        pkg.embedding_bag_pooled(torch.zeros(3, dtype=torch.int64), torch.zeros(5, dtype=torch.int64), [(q,)])
