@@ -10,6 +10,13 @@ not find each other's rows in L2 / MALL.
 the int8 rows with their fp32 scales (online_best/infer.py:904-942); the algorithmic bytes count
 1 byte per element plus the 4-byte scale of each looked-up row.
 
+`--stage h2d` measures the step end to end from host memory (online_best/infer.py:742-779): each
+step moves one flat-layout batch (int64 ids and offsets in pageable host memory, as the collate
+leaves them) to the GPU and pools it with the reference launch (one shared table, sum), through
+(a) the reference's `.to(device, non_blocking=True)`, (b) the pinned, double-buffered InputStager
+with int64 inputs, (c) the same with ids and offsets narrowed to int32 on the host. The line
+reports bags/s per variant, the copy-only and pool-only times, and the bytes moved per batch.
+
 `--stage layernorm` times the encoder's input LayerNorm instead (online_best/infer.py:1061-1076):
 the workload's batches are pooled once, and each step normalises one pooled block
 [B, sum(D)] (rows/s; roofline bytes = the block read and written plus gamma and beta).
@@ -100,6 +107,112 @@ def cpu_baseline(wl, tables_dev, seconds):
                       f"F.embedding_bag per field (oracle/cpu_loops.py), {wl.table_dtype} tables in host memory"}
 
 
+def bench_h2d(args, pkg, wls, dev):
+    """End-to-end steps from host flat-layout batches: transfer + the reference pooling launch."""
+    import numpy as np
+    import torch
+
+    wl0 = wls[0]
+    F, B, D = wl0.num_fields, wl0.batch, wl0.dims[0]
+    V = max(wl0.vocab)
+    host = []
+    for wl in wls:
+        off = wl.offsets
+        ro = np.stack([off[f * B:(f + 1) * B + 1] - off[f * B] for f in range(F)]).reshape(-1)
+        vo = off[0:F * B:B].copy()
+        host.append({"_flat_values": torch.from_numpy(wl.values.copy()), "_flat_row_offsets": torch.from_numpy(ro),
+                     "_val_offsets": torch.from_numpy(vo)})
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    weight = torch.empty((V, D), dtype=wl0.table_dtype, device=dev)
+    weight.normal_(0.0, 0.01, generator=g)
+    out = torch.empty((B, F * D), dtype=wl0.table_dtype, device=dev)
+    max_nnz = max(h["_flat_values"].numel() for h in host)
+    n = len(host)
+
+    def pool(db):
+        pkg.fused_all_slots_embedding(db["_flat_values"], db["_val_offsets"], db["_flat_row_offsets"], weight, out,
+                                      B, D, V - 1)
+
+    def run(step, K, W):
+        for i in range(W):
+            step(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(K):
+            step(W + i)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / K
+
+    results = {}
+
+    def reference(i):
+        pool(pkg.move_model_inputs_to_device(host[i % n], dev, F))
+
+    log("reference transfer (.to(device, non_blocking=True) of pageable int64)")
+    results["reference_pageable_int64"] = run(reference, args.steps, args.warmup)
+    # host batches whose producer already emits int32 (saturated) ids and offsets
+    host32 = []
+    for h in host:
+        h32 = {}
+        for k, t in h.items():
+            d = torch.empty(t.numel(), dtype=torch.int32)
+            pkg._capi.check(pkg._capi.lib().cti_ebag_narrow_ids(t.data_ptr(), t.numel(), d.data_ptr(), 16))
+            h32[k] = d
+        host32.append(h32)
+    for name, compact, src in (("pinned_int64_overlapped", False, host), ("pinned_int32_overlapped", True, host),
+                               ("pinned_int32_from_int32_overlapped", True, host32)):
+        stager = pkg.InputStager(max_nnz, F, B, dev, depth=2, compact=compact)
+
+        def staged(i, stager=stager, src=src):
+            db = pkg.move_model_inputs_to_device(src[i % n], dev, F, stager=stager)
+            pool(db)
+            stager.release(db)
+
+        def copy_only(i, stager=stager, src=src):
+            stager.release(stager.stage(src[i % n]))
+
+        log(name)
+        results[name] = run(staged, args.steps, args.warmup)
+        results[name.replace("overlapped", "copy_only")] = run(copy_only, args.steps, args.warmup)
+        torch.cuda.synchronize()
+        del stager
+    # the DMA alone: host data already in pinned buffers
+    for width, dt in ((8, torch.int64), (4, torch.int32)):
+        hbuf = torch.empty(max_nnz + F * (B + 2), dtype=dt, pin_memory=True)
+        dbuf = torch.empty_like(hbuf, device=dev)
+        results[f"dma_only_int{width * 8}"] = run(lambda i: dbuf.copy_(hbuf, non_blocking=True), args.steps,
+                                                  args.warmup)
+        del hbuf, dbuf
+    resident = [pkg.move_model_inputs_to_device(h, dev, F) for h in host]
+    results["pool_only_resident_int64"] = run(lambda i: pool(resident[i % n]), args.steps, args.warmup)
+    bags = wl0.num_bags
+    nnz_mean = float(np.mean([h["_flat_values"].numel() for h in host]))
+    bytes64 = 8 * (nnz_mean + F * (B + 1) + F)
+    best = min(("reference_pageable_int64", "pinned_int64_overlapped", "pinned_int32_overlapped",
+                "pinned_int32_from_int32_overlapped"), key=lambda k: results[k])
+    rec = {
+        "metric": "end-to-end pooled bags/sec from host flat-layout batches (H2D + pooling), B=4096x28 fields, D=128 bf16",
+        "value": bags / results[best],
+        "unit": "bags/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": results[best] * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": f"synthetic: {n} seeded index sets rotated, host batches in pageable int64 tensors",
+        "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}; one shared table "
+                               f"[{V}, {D}], sum (the reference launch)", "best_variant": best},
+        "us_per_step": {k: v * 1e6 for k, v in results.items()},
+        "bags_per_s": {k: bags / v for k, v in results.items()},
+        "h2d_bytes_per_batch": {"int64": bytes64, "int32": bytes64 / 2},
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def bench_layernorm(args, pkg, plan, inputs, wl0, dev):
     """Time the input LayerNorm over pooled blocks of the workload (one block per step, rotated)."""
     import torch
@@ -156,8 +269,9 @@ def main():
     ap.add_argument("--long-threshold", type=int, default=0)
     ap.add_argument("--bins", action="store_true", help="run the device length-binning pass")
     ap.add_argument("--block-threshold", type=int, default=0)
-    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm"],
-                    help="time the pooling step (default) or the input LayerNorm over pooled blocks")
+    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d"],
+                    help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
+                         "step end to end from host batches")
     ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times (scales rocprofv3 FETCH/WRITE_SIZE) and exit")
@@ -193,6 +307,8 @@ def main():
     log(f"workload {args.workload}: generating {args.sets} index sets")
     wls = [W.make(args.workload, seed=s) for s in range(1, args.sets + 1)]
     wl0 = wls[0]
+    if args.stage == "h2d":
+        return bench_h2d(args, pkg, wls, dev)
     log("filling tables on the device")
     tables = W.make_tables(wl0, dev, seed=0)
     inputs = [W.to_device(wl, dev) for wl in wls]

@@ -11,11 +11,14 @@ Public surface:
   RepEncoder                 the reference module with the fused step and LayerNorm on this path
   collate_flat_layout, prebuild_flat_layout   host builders of the flat layout
   pack_slots, merge_batches                   GPU builders of the flat layout
+  InputStager, move_model_inputs_to_device    pinned, int32-compacted, overlapped transfer of
+                                              host batches to the GPU
 """
 from . import workloads
 from ._capi import EbagError, lib as load_library
 from .encoder import RepEncoder
 from .layout import collate_flat_layout, merge_batches, pack_slots, prebuild_flat_layout
+from .staging import InputStager, move_model_inputs_to_device
 from .ops import (PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_all_slots_embedding_int8,
                   fused_embedding, layer_norm, quantize_embedding_int8)
 
@@ -27,6 +30,8 @@ __all__ = [
     "prebuild_flat_layout",
     "pack_slots",
     "merge_batches",
+    "InputStager",
+    "move_model_inputs_to_device",
     "embedding_bag_pooled",
     "PooledEmbedding",
     "fused_all_slots_embedding",

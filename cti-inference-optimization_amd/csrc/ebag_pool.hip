@@ -117,8 +117,8 @@ struct FieldDesc {
 
 struct PoolParams {
   const void* values;
-  const int64_t* offsets;   // bag offsets, field f starts at offsets + gidx * offsets_stride
-  const int64_t* val_base;  // optional per-field base added to offsets (reference layout)
+  const void* offsets;      // bag offsets, field f starts at offsets + gidx * offsets_stride
+  const void* val_base;     // optional per-field base added to offsets (reference layout)
   char* out;
   int64_t nnz;
   int64_t offsets_stride;
@@ -133,6 +133,7 @@ struct PoolParams {
   int32_t tiles_per_field;  // every field of a launch has the same number of tiles
   int32_t pooling;          // CTI_EBAG_SUM / CTI_EBAG_MEAN
   int32_t idx32;
+  int32_t off32;            // offsets and val_base are int32 (else int64)
   int32_t buffer_ok;        // every field's span_bytes is set: rows are read with buffer loads
   FieldDesc f[kMaxFields];
 };
@@ -190,12 +191,16 @@ __device__ __forceinline__ int64_t load_index(const PoolParams& p, int64_t e) {
                  : static_cast<const int64_t*>(p.values)[e];
 }
 
+__device__ __forceinline__ int64_t load_offset(const PoolParams& p, const void* a, int64_t i) {
+  return p.off32 ? static_cast<int64_t>(static_cast<const int32_t*>(a)[i]) : static_cast<const int64_t*>(a)[i];
+}
+
 __device__ __forceinline__ void bag_range(const PoolParams& p, int gidx, int64_t b,
                                           int64_t& start, int64_t& end) {
-  const int64_t* o = p.offsets + static_cast<int64_t>(gidx) * p.offsets_stride + b;
-  const int64_t base = p.val_base ? p.val_base[gidx] : 0;
-  start = clamp_i64(base + o[0], 0, p.nnz);
-  end = clamp_i64(base + o[1], start, p.nnz);
+  const int64_t i = static_cast<int64_t>(gidx) * p.offsets_stride + b;
+  const int64_t base = p.val_base ? load_offset(p, p.val_base, gidx) : 0;
+  start = clamp_i64(base + load_offset(p, p.offsets, i), 0, p.nnz);
+  end = clamp_i64(base + load_offset(p, p.offsets, i + 1), start, p.nnz);
 }
 
 // Row shape of one kernel instance.
@@ -684,8 +689,9 @@ struct Job {
   const void* values;
   int32_t idx32;
   int64_t nnz;
-  const int64_t* offsets;
-  const int64_t* val_base;
+  const void* offsets;
+  const void* val_base;
+  int32_t off32;
   int64_t offsets_stride;
   int64_t batch;
   int32_t num_fields;
@@ -748,6 +754,7 @@ int run_job(const Job& j, hipStream_t stream) {
       p.batch = j.batch;
       p.pooling = j.pooling;
       p.idx32 = j.idx32;
+      p.off32 = j.off32;
       if (v == kVarGeneric) p.sub_threshold = kNoLimit;
       else if (j.sub_threshold == 0) p.sub_threshold = default_sub_threshold(v);
       else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;
@@ -811,10 +818,14 @@ namespace cti {
 namespace {
 
 // The reference-layout launch (one shared table, slot-local offsets, sum pooling) for any table
-// type; `scale` is the int8 table's per-row scale.
-int run_all_slots(const int64_t* values, const int64_t* val_offsets, const int64_t* row_offsets, const void* weight,
-                  const float* scale, int32_t tdt, void* out, int32_t odt, int64_t batch_size, int32_t num_slots,
-                  int32_t emb_dim, int64_t max_idx, int64_t nnz, void* stream) {
+// type and index / offset width; `scale` is the int8 table's per-row scale.
+int run_all_slots(const void* values, int32_t index_type, const void* val_offsets, const void* row_offsets,
+                  int32_t offset_type, const void* weight, const float* scale, int32_t tdt, void* out, int32_t odt,
+                  int64_t batch_size, int32_t num_slots, int32_t emb_dim, int64_t max_idx, int64_t nnz, void* stream) {
+  if (index_type != CTI_EBAG_I64 && index_type != CTI_EBAG_I32)
+    return set_error(CTI_EBAG_EINVAL, "unknown index type code %d", index_type);
+  if (offset_type != CTI_EBAG_I64 && offset_type != CTI_EBAG_I32)
+    return set_error(CTI_EBAG_EINVAL, "unknown offset type code %d", offset_type);
   if (batch_size < 0) return set_error(CTI_EBAG_EINVAL, "batch_size must be >= 0 (got %lld)", (long long)batch_size);
   if (num_slots < 0) return set_error(CTI_EBAG_EINVAL, "num_slots must be >= 0 (got %d)", num_slots);
   if (emb_dim < 1) return set_error(CTI_EBAG_EINVAL, "emb_dim must be >= 1 (got %d)", emb_dim);
@@ -836,9 +847,11 @@ int run_all_slots(const int64_t* values, const int64_t* val_offsets, const int64
   Job j;
   memset(&j, 0, sizeof(j));
   j.values = values;
+  j.idx32 = index_type == CTI_EBAG_I32;
   j.nnz = nnz;
   j.offsets = row_offsets;
   j.val_base = val_offsets;
+  j.off32 = offset_type == CTI_EBAG_I32;
   j.offsets_stride = batch_size + 1;
   j.batch = batch_size;
   j.num_fields = num_slots;
@@ -860,8 +873,8 @@ extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* va
                                         int64_t max_idx, int64_t nnz, void* stream) {
   clear_error();
   if (!dtype_ok(dtype)) return set_error(CTI_EBAG_EINVAL, "unknown dtype code %d", dtype);
-  return run_all_slots(values, val_offsets, row_offsets, weight, nullptr, dtype, out, dtype, batch_size, num_slots,
-                       emb_dim, max_idx, nnz, stream);
+  return run_all_slots(values, CTI_EBAG_I64, val_offsets, row_offsets, CTI_EBAG_I64, weight, nullptr, dtype, out, dtype,
+                       batch_size, num_slots, emb_dim, max_idx, nnz, stream);
 }
 
 extern "C" int cti_ebag_fused_all_slots_int8(const int64_t* values, const int64_t* val_offsets,
@@ -871,8 +884,22 @@ extern "C" int cti_ebag_fused_all_slots_int8(const int64_t* values, const int64_
                                              void* stream) {
   clear_error();
   if (!dtype_ok(out_dtype)) return set_error(CTI_EBAG_EINVAL, "unknown output dtype code %d", out_dtype);
-  return run_all_slots(values, val_offsets, row_offsets, weight_int8, scale, CTI_EBAG_I8, out, out_dtype, batch_size,
-                       num_slots, emb_dim, max_idx, nnz, stream);
+  return run_all_slots(values, CTI_EBAG_I64, val_offsets, row_offsets, CTI_EBAG_I64, weight_int8, scale, CTI_EBAG_I8,
+                       out, out_dtype, batch_size, num_slots, emb_dim, max_idx, nnz, stream);
+}
+
+extern "C" int cti_ebag_fused_all_slots_typed(const void* values, int32_t index_type, const void* val_offsets,
+                                              const void* row_offsets, int32_t offset_type, const void* weight,
+                                              int32_t table_dtype, const float* scale, void* out, int32_t out_dtype,
+                                              int64_t batch_size, int32_t num_slots, int32_t emb_dim, int64_t max_idx,
+                                              int64_t nnz, void* stream) {
+  clear_error();
+  if (!dtype_ok(table_dtype) && table_dtype != CTI_EBAG_I8)
+    return set_error(CTI_EBAG_EINVAL, "unknown table dtype code %d", table_dtype);
+  if (!dtype_ok(out_dtype)) return set_error(CTI_EBAG_EINVAL, "unknown output dtype code %d", out_dtype);
+  return run_all_slots(values, index_type, val_offsets, row_offsets, offset_type, weight,
+                       table_dtype == CTI_EBAG_I8 ? scale : nullptr, table_dtype, out, out_dtype, batch_size, num_slots,
+                       emb_dim, max_idx, nnz, stream);
 }
 
 extern "C" int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fields) {

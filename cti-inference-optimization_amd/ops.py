@@ -114,14 +114,22 @@ def quantize_embedding_int8(weight: torch.Tensor):
 
 
 def _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev):
+    """Validate a flat-layout batch; return the (index, offset) type codes. Ids may be int64 or
+    int32; val_offsets and flat_row_offsets share one type, int64 or int32."""
     for name, t in (("flat_values", flat_values), ("val_offsets", val_offsets),
                     ("flat_row_offsets", flat_row_offsets), ("out", out)):
         _require_device_tensor(name, t, dev)
         _require_contiguous(name, t)
     for name, t in (("flat_values", flat_values), ("val_offsets", val_offsets),
                     ("flat_row_offsets", flat_row_offsets)):
-        if t.dtype != torch.int64:
-            raise TypeError(f"{name} must be int64 (got {t.dtype})")
+        if t.dtype not in (torch.int64, torch.int32):
+            raise TypeError(f"{name} must be int64 or int32 (got {t.dtype})")
+    return _capi.index_code(flat_values.dtype), _capi.index_code(flat_row_offsets.dtype)
+
+
+def _same_offset_type(val_offsets: torch.Tensor, flat_row_offsets: torch.Tensor) -> torch.Tensor:
+    """val_offsets in flat_row_offsets' dtype (the reference widens only val_offsets, :747)."""
+    return val_offsets if val_offsets.dtype == flat_row_offsets.dtype else val_offsets.to(flat_row_offsets.dtype)
 
 
 def fused_all_slots_embedding_int8(
@@ -146,7 +154,8 @@ def fused_all_slots_embedding_int8(
     """
     dev = weight_int8.device
     _require_device_tensor("weight_int8", weight_int8)
-    _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
+    icode, ocode = _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
+    val_offsets = _same_offset_type(val_offsets, flat_row_offsets)
     _require_device_tensor("scale", scale, dev)
     _require_contiguous("weight_int8", weight_int8)
     _require_contiguous("scale", scale)
@@ -168,10 +177,17 @@ def fused_all_slots_embedding_int8(
     if out.numel() != batch_size * num_slots * emb_dim or (out.dim() >= 1 and out.shape[0] != batch_size):
         raise ValueError(f"out has shape {tuple(out.shape)}, expected ({batch_size}, {num_slots * emb_dim})")
     with torch.cuda.device(dev):
-        _capi.check(_capi.lib().cti_ebag_fused_all_slots_int8(
-            flat_values.data_ptr(), val_offsets.data_ptr(), flat_row_offsets.data_ptr(), weight_int8.data_ptr(),
-            scale.data_ptr(), out.data_ptr(), _capi.dtype_code(out.dtype), batch_size, num_slots, emb_dim, max_idx,
-            flat_values.numel(), _capi.current_stream_handle(dev)))
+        stream = _capi.current_stream_handle(dev)
+        if icode == _capi.I64 and ocode == _capi.I64:
+            _capi.check(_capi.lib().cti_ebag_fused_all_slots_int8(
+                flat_values.data_ptr(), val_offsets.data_ptr(), flat_row_offsets.data_ptr(), weight_int8.data_ptr(),
+                scale.data_ptr(), out.data_ptr(), _capi.dtype_code(out.dtype), batch_size, num_slots, emb_dim,
+                max_idx, flat_values.numel(), stream))
+        else:
+            _capi.check(_capi.lib().cti_ebag_fused_all_slots_typed(
+                flat_values.data_ptr(), icode, val_offsets.data_ptr(), flat_row_offsets.data_ptr(), ocode,
+                weight_int8.data_ptr(), _capi.I8, scale.data_ptr(), out.data_ptr(), _capi.dtype_code(out.dtype),
+                batch_size, num_slots, emb_dim, max_idx, flat_values.numel(), stream))
     return out
 
 
@@ -191,6 +207,8 @@ def fused_all_slots_embedding(
       flat_values       int64 [nnz]        field-major sign ids (online_best/infer.py:471)
       val_offsets       int64 [S]          slot starts in flat_values (online_best/infer.py:473)
       flat_row_offsets  int64 [S*(B+1)]    per-slot local offsets (online_best/infer.py:472)
+      (ids and offsets may also be int32, as the Triton kernel specialises on its pointer dtypes;
+      the int32 forms give the same result bit for bit)
       weight            [V, emb_dim]       shared table (fp32 / bf16 / fp16), contiguous
       out               [B, S*emb_dim]     caller-allocated, weight's dtype (online_best/infer.py:1050)
       batch_size        B
@@ -200,7 +218,8 @@ def fused_all_slots_embedding(
     """
     dev = weight.device
     _require_device_tensor("weight", weight)
-    _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
+    icode, ocode = _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
+    val_offsets = _same_offset_type(val_offsets, flat_row_offsets)
     if weight.dim() != 2:
         raise ValueError(f"weight must be 2-D [V, D], got shape {tuple(weight.shape)}")
     _require_contiguous("weight", weight)
@@ -226,10 +245,17 @@ def fused_all_slots_embedding(
     lib = _capi.lib()
     with torch.cuda.device(dev):
         stream = _capi.current_stream_handle(dev)
-        _capi.check(lib.cti_ebag_fused_all_slots(
-            flat_values.data_ptr(), val_offsets.data_ptr(), flat_row_offsets.data_ptr(),
-            weight.data_ptr(), _capi.dtype_code(weight.dtype), out.data_ptr(),
-            batch_size, num_slots, emb_dim, max_idx, flat_values.numel(), stream))
+        if icode == _capi.I64 and ocode == _capi.I64:
+            _capi.check(lib.cti_ebag_fused_all_slots(
+                flat_values.data_ptr(), val_offsets.data_ptr(), flat_row_offsets.data_ptr(),
+                weight.data_ptr(), _capi.dtype_code(weight.dtype), out.data_ptr(),
+                batch_size, num_slots, emb_dim, max_idx, flat_values.numel(), stream))
+        else:
+            code = _capi.dtype_code(weight.dtype)
+            _capi.check(lib.cti_ebag_fused_all_slots_typed(
+                flat_values.data_ptr(), icode, val_offsets.data_ptr(), flat_row_offsets.data_ptr(), ocode,
+                weight.data_ptr(), code, None, out.data_ptr(), code, batch_size, num_slots, emb_dim, max_idx,
+                flat_values.numel(), stream))
     return out
 
 

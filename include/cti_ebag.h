@@ -198,9 +198,57 @@ int cti_ebag_fused_all_slots_int8(const int64_t* values, const int64_t* val_offs
                                   void* stream);
 
 /*
- * Row quantisation of a table to int8, as quantize_embedding_int8 (online_best/infer.py:895-901):
- *   m = max_j |w[r, j]| (fp32), s = max(m / 127, 1e-8) (fp32), q[r, j] = clamp(rint(w / s), -128, 127)
- * with fp32 IEEE division and round half to even, bit for bit.
+ * Reference-layout entry point for any index / offset width and table type: the launch above
+ * (or its int8 form) with
+ *   values       [nnz] of `index_type` (CTI_EBAG_I64 / CTI_EBAG_I32)
+ *   val_offsets  [num_slots], row_offsets [num_slots*(B+1)], both of `offset_type` (I64 / I32)
+ *   table_dtype  F32 / BF16 / F16, or I8 with `scale` fp32 [max_idx+1] (else ignored)
+ *   out          [B, num_slots*emb_dim] of `out_dtype`
+ * The Triton kernel specialises on the dtypes of its pointer arguments, so the reference launch
+ * (online_best/infer.py:1052-1059) accepts int32 inputs the same way; the int32 forms halve the
+ * input bytes a caller moves to the device (online_best/infer.py:742-779). Ids are widened and
+ * clamped on the device; results equal the int64 call's bit for bit.
+ */
+int cti_ebag_fused_all_slots_typed(const void* values, int32_t index_type, const void* val_offsets,
+                                   const void* row_offsets, int32_t offset_type, const void* weight,
+                                   int32_t table_dtype, const float* scale, void* out, int32_t out_dtype,
+                                   int64_t batch_size, int32_t num_slots, int32_t emb_dim, int64_t max_idx,
+                                   int64_t nnz, void* stream);
+
+/*
+ * Host-side compaction of sign ids for the transfer to the device (replaces the int64
+ * `.to(device, non_blocking=True)` of `_flat_values` at online_best/infer.py:745-746; the comment
+ * at :744 names the int32 form). `src` and `dst` are HOST pointers (dst typically pinned):
+ *   dst[i] = saturate_int32(src[i]),  i < n,
+ * using up to `num_threads` threads. Saturation keeps the pooled result identical to the int64
+ * ids' (every table has < 2^31 rows, so clamp(saturate(v)) == clamp(v)). Synchronous.
+ */
+int cti_ebag_narrow_ids(const int64_t* src, int64_t n, int32_t* dst, int32_t num_threads);
+
+/*
+ * Host side of one batch's transfer (online_best/infer.py:742-779 moves each tensor with its own
+ * `.to(device)`): the `n_parts` host arrays src[p] (`src_type[p]` I64 / I32, counts[p] elements)
+ * are converted to `dst_type` (I32: saturating narrow as in cti_ebag_narrow_ids; I64: widened or
+ * copied) into ONE contiguous region of the pinned host buffer `pinned` (part p starts at
+ * cti_ebag_stage_offset(counts, n_parts, dst_type, p), 256-byte aligned), using up to
+ * `num_threads` host threads, and then one hipMemcpyAsync sends the region to `device_dst` (same
+ * layout) on `stream`. Returns once the copy is enqueued; `pinned` must not be rewritten until
+ * the copy has run (order on `stream`). At most 8 parts.
+ */
+int cti_ebag_stage_copy(const void* const* src, const int32_t* src_type, const int64_t* counts,
+                        int32_t n_parts, int32_t dst_type, void* pinned, int64_t pinned_bytes,
+                        void* device_dst, int32_t num_threads, void* stream);
+
+/* Byte offset of part `part` in the staging layout above (part == n_parts: total bytes); -1 for
+ * bad arguments. Host pointers only. */
+int64_t cti_ebag_stage_offset(const int64_t* counts, int32_t n_parts, int32_t dst_type, int32_t part);
+
+/*
+ * Row quantisation of a table to int8, quantize_embedding_int8 (online_best/infer.py:895-901) as
+ * torch evaluates it on the device:
+ *   m = max_j |w[r, j]| (fp32), s = max(m * RN32(1/127), 1e-8) (the division by the Python
+ *   scalar 127.0 is a multiply by its fp32 reciprocal there), q[r, j] = clamp(rint(w / s), -128, 127)
+ * with IEEE fp32 division and round half to even, bit for bit.
  *   weight  [rows, row_stride] of `dtype` (F32/BF16/F16), first `dim` columns used
  *   q       int8 [rows, dim] (contiguous), scale fp32 [rows]. Tables must be finite.
  */

@@ -21,7 +21,8 @@ def test_header_declares_the_entry_points():
     names = declared_functions()
     for n in ("cti_ebag_fused_all_slots", "cti_ebag_forward", "cti_ebag_pack_slots", "cti_ebag_merge_batches",
               "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version", "cti_ebag_layernorm",
-              "cti_ebag_fused_all_slots_int8", "cti_ebag_quantize_int8"):
+              "cti_ebag_fused_all_slots_int8", "cti_ebag_quantize_int8", "cti_ebag_fused_all_slots_typed",
+              "cti_ebag_narrow_ids", "cti_ebag_stage_copy", "cti_ebag_stage_offset"):
         assert n in names
 
 
@@ -226,3 +227,56 @@ def test_int8_python_wrappers_validate_before_any_launch(pkg):
                                  [(q, torch.ones(10))])
     with pytest.raises(ValueError, match="pair"):
         pkg.embedding_bag_pooled(torch.zeros(3, dtype=torch.int64), torch.zeros(5, dtype=torch.int64), [(q,)])
+
+
+@pytest.mark.parametrize("n,threads", [(0, 1), (1, 4), (1000, 1), (200_003, 3), (1 << 20, 16)])
+def test_narrow_ids_saturates(pkg, n, threads):
+    """Host-side int64 -> int32 id compaction: saturating, so the device clamp sees the same row."""
+    import numpy as np
+
+    rng = np.random.default_rng(n)
+    src = rng.integers(-(2 ** 40), 2 ** 40, n, dtype=np.int64)
+    if n >= 8:
+        src[:8] = [np.iinfo(np.int64).min, np.iinfo(np.int64).max, 2 ** 31, 2 ** 31 - 1, -(2 ** 31), -(2 ** 31) - 1, 0, -1]
+    dst = np.full(n, 7, dtype=np.int32)
+    rc = pkg._capi.lib().cti_ebag_narrow_ids(src.ctypes.data if n else None, n, dst.ctypes.data if n else None,
+                                               threads)
+    assert rc == pkg._capi.OK
+    want = np.clip(src, -(2 ** 31), 2 ** 31 - 1).astype(np.int32)
+    assert np.array_equal(dst, want)
+    # the property the device relies on: clamping the narrowed id gives the int64 id's row
+    for rows in (1, 5_000_000, 2 ** 31 - 1):
+        assert np.array_equal(np.clip(dst.astype(np.int64), 0, rows - 1), np.clip(src, 0, rows - 1))
+
+
+def test_narrow_ids_rejects_bad_arguments(pkg):
+    c = pkg._capi
+    f = c.lib().cti_ebag_narrow_ids
+    assert f(None, 10, 64, 1) == c.EINVAL
+    assert f(64, -1, 64, 1) == c.EINVAL
+    assert f(64, 10, 64, 0) == c.EINVAL and "num_threads" in c.last_error()
+
+
+def test_stage_offsets_layout(pkg):
+    c = pkg._capi
+    f = c.lib().cti_ebag_stage_offset
+    counts = (ctypes.c_int64 * 3)(1000, 28 * 4097, 28)
+    assert [f(counts, 3, c.I32, p) for p in range(4)] == [0, 4096, 4096 + 459008, 4096 + 459008 + 256]
+    assert [f(counts, 3, c.I64, p) for p in range(4)] == [0, 8192, 8192 + 917760, 8192 + 917760 + 256]
+    assert f(counts, 3, 9, 1) == -1 and f(counts, 3, c.I32, 4) == -1 and f(None, 3, c.I32, 1) == -1
+
+
+def test_stage_copy_rejects_bad_arguments(pkg):
+    c = pkg._capi
+    f = c.lib().cti_ebag_stage_copy
+    src = (ctypes.c_void_p * 2)(64, 64)
+    st = (ctypes.c_int32 * 2)(c.I64, c.I64)
+    cnt = (ctypes.c_int64 * 2)(10, 10)
+    assert f(src, st, cnt, 9, c.I32, 64, 1 << 20, 64, 4, None) == c.EINVAL
+    assert f(src, st, cnt, 2, 7, 64, 1 << 20, 64, 4, None) == c.EINVAL
+    assert f(src, st, cnt, 2, c.I32, 64, 100, 64, 4, None) == c.EINVAL and "staging bytes" in c.last_error()
+    assert f(src, st, cnt, 2, c.I32, None, 1 << 20, 64, 4, None) == c.EINVAL
+    bad = (ctypes.c_int32 * 2)(c.I64, 5)
+    assert f(src, bad, cnt, 2, c.I32, 64, 1 << 20, 64, 4, None) == c.EINVAL
+    zero = (ctypes.c_int64 * 2)(0, 0)
+    assert f(src, st, zero, 2, c.I32, None, 0, None, 4, None) == c.OK

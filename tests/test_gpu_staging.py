@@ -1,0 +1,121 @@
+"""int32 inputs and the host -> device staging path on the GPU.
+
+Bar: the pooled output from int32 ids / offsets, and from batches moved by InputStager (pinned,
+int32-compacted, double-buffered), is bit-identical to the int64 path's, including ids outside
+the int32 range (saturated on the host, clamped on the device).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+S, V, D = 28, 3000, 128
+
+
+def host_batch(rng, B, max_len=12, wide_ids=True):
+    L = rng.integers(0, max_len + 1, (S, B))
+    L[:, min(1, B - 1)] = 0
+    ro = np.zeros((S, B + 1), np.int64)
+    np.cumsum(L, axis=1, out=ro[:, 1:])
+    vo = np.concatenate([[0], np.cumsum(L.sum(axis=1))[:-1]]).astype(np.int64)
+    v = rng.integers(0, V, int(L.sum())).astype(np.int64)
+    if wide_ids and v.size >= 6:
+        v[:6] = [2 ** 31, -(2 ** 31) - 5, np.iinfo(np.int64).max, np.iinfo(np.int64).min, 2 ** 40 + 3, -1]
+    return {"_flat_values": torch.from_numpy(v), "_flat_row_offsets": torch.from_numpy(ro.reshape(-1)),
+            "_val_offsets": torch.from_numpy(vo)}, B
+
+
+def pool(pkg, dev_batch, weight, B):
+    out = torch.empty((B, S * D), dtype=weight.dtype, device=weight.device)
+    return pkg.fused_all_slots_embedding(dev_batch["_flat_values"], dev_batch["_val_offsets"],
+                                         dev_batch["_flat_row_offsets"], weight, out, B, D, V - 1)
+
+
+@pytest.fixture(scope="module")
+def weight(dev):
+    g = torch.Generator(device="cpu").manual_seed(1)
+    return torch.randn(V, D, generator=g).to(torch.bfloat16).to(dev)
+
+
+@pytest.mark.parametrize("vt,ot", [(torch.int32, torch.int32), (torch.int32, torch.int64), (torch.int64, torch.int32)])
+def test_int32_layouts_match_int64(pkg, dev, weight, vt, ot):
+    rng = np.random.default_rng(3)
+    hb, B = host_batch(rng, 77, wide_ids=False)
+    ref = pool(pkg, {k: t.to(dev) for k, t in hb.items()}, weight, B)
+    narrow = {"_flat_values": hb["_flat_values"].to(vt).to(dev), "_flat_row_offsets": hb["_flat_row_offsets"].to(ot).to(dev),
+              "_val_offsets": hb["_val_offsets"].to(ot).to(dev)}
+    got = pool(pkg, narrow, weight, B)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_int32_mixed_offset_types_and_int8(pkg, dev, weight):
+    rng = np.random.default_rng(4)
+    hb, B = host_batch(rng, 50, wide_ids=False)
+    q, s = pkg.quantize_embedding_int8(weight)
+    outs = []
+    for vt, rt, bt in ((torch.int64, torch.int64, torch.int64), (torch.int32, torch.int32, torch.int64)):
+        out = torch.empty((B, S * D), dtype=torch.bfloat16, device=dev)
+        pkg.fused_all_slots_embedding_int8(hb["_flat_values"].to(vt).to(dev), hb["_val_offsets"].to(bt).to(dev),
+                                           hb["_flat_row_offsets"].to(rt).to(dev), q, s, out, B, D, V - 1)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
+@pytest.mark.parametrize("compact", [True, False])
+@pytest.mark.parametrize("depth", [1, 2, 3])
+def test_stager_pipeline_matches_direct_transfer(pkg, dev, weight, compact, depth):
+    print(f"stager compact={compact} depth={depth}", flush=True)
+    rng = np.random.default_rng(depth * 2 + compact)
+    batches = [host_batch(rng, int(rng.integers(1, 200))) for _ in range(7)]
+    max_nnz = max(b["_flat_values"].numel() for b, _ in batches)
+    stager = pkg.InputStager(max_nnz, S, 200, dev, depth=depth, compact=compact)
+    got = []
+    for hb, B in batches:
+        staged = pkg.move_model_inputs_to_device(hb, dev, S, stager=stager)
+        if compact:
+            assert staged["_flat_values"].dtype == torch.int32
+        got.append(pool(pkg, staged, weight, B).clone())
+        stager.release(staged)
+    torch.cuda.synchronize()
+    for (hb, B), g in zip(batches, got):
+        ref = pool(pkg, pkg.move_model_inputs_to_device(hb, dev, S), weight, B)
+        torch.cuda.synchronize()
+        assert torch.equal(g.view(torch.int16), ref.view(torch.int16))
+
+
+def test_stager_requires_release(pkg, dev, weight):
+    rng = np.random.default_rng(9)
+    hb, B = host_batch(rng, 10)
+    stager = pkg.InputStager(hb["_flat_values"].numel(), S, 10, dev, depth=2)
+    a = stager.stage(hb)
+    b = stager.stage(hb)
+    with pytest.raises(RuntimeError, match="release"):
+        stager.stage(hb)
+    pool(pkg, a, weight, B)
+    stager.release(a)
+    c = stager.stage(hb)
+    pool(pkg, b, weight, B)
+    pool(pkg, c, weight, B)
+    stager.release(b)
+    stager.release(c)
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError, match="holds"):
+        big = dict(hb)
+        big["_flat_values"] = torch.zeros(hb["_flat_values"].numel() + 1, dtype=torch.int64)
+        stager.stage(big)
+
+
+def test_per_slot_pairs_are_packed_on_device(pkg, dev, weight):
+    rng = np.random.default_rng(11)
+    hb, B = host_batch(rng, 30, wide_ids=False)
+    v, ro, vo = hb["_flat_values"].numpy(), hb["_flat_row_offsets"].numpy().reshape(S, B + 1), hb["_val_offsets"].numpy()
+    pairs = {}
+    for s in range(S):
+        end = vo[s + 1] if s + 1 < S else v.size
+        pairs[s + 1] = (torch.from_numpy(v[vo[s]:end].copy()), torch.from_numpy(ro[s].copy()))
+    moved = pkg.move_model_inputs_to_device(pairs, dev, S)
+    for k in ("_flat_values", "_flat_row_offsets", "_val_offsets"):
+        assert torch.equal(moved[k].cpu(), hb[k])
