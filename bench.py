@@ -72,8 +72,11 @@ def traffic_from_profiles(workload):
 
 
 def cpu_baseline(wl, tables_dev, seconds):
-    """Time the oracle's F.embedding_bag loop on host tables holding the rows this batch reads
-    (full-size tables, untouched rows left as zero pages), for about `seconds` of CPU work."""
+    """Time the reference's CPU pooling on this host, on host tables holding the rows this batch
+    reads (full-size tables, untouched rows left as zero pages): the oracle's F.embedding_bag loop
+    (the reported baseline) and the literal baseline loop (clamp + F.embedding + segment_reduce +
+    cat, baseline/infer.py:256-263), each pass timed separately for about `seconds` / 2 of CPU work
+    (at least 5 passes); medians are reported."""
     import numpy as np
     import torch
 
@@ -94,17 +97,25 @@ def cpu_baseline(wl, tables_dev, seconds):
         host.append(h)
     values = torch.from_numpy(wl.values)
     offsets = torch.from_numpy(wl.offsets)
-    cpu_loops.embedding_bag_loop(values, offsets, host, wl.pooling, wl.batch)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        cpu_loops.embedding_bag_loop(values, offsets, host, wl.pooling, wl.batch)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 1000:
-            break
-    return {"value": n * wl.num_bags / el, "unit": "bags/s", "cores": threads, "kind": "port",
-            "sample": f"{n} full passes of the timed batch ({wl.num_bags} bags each) in {el:.1f} s through "
-                      f"F.embedding_bag per field (oracle/cpu_loops.py), {wl.table_dtype} tables in host memory"}
+
+    def timed(loop):
+        loop(values, offsets, host, wl.pooling, wl.batch)  # warm-up
+        times, t_start = [], time.perf_counter()
+        while len(times) < 5 or (time.perf_counter() - t_start < seconds / 2 and len(times) < 100_000):
+            t0 = time.perf_counter()
+            loop(values, offsets, host, wl.pooling, wl.batch)
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times)), len(times), time.perf_counter() - t_start
+
+    med_bag, n_bag, el_bag = timed(cpu_loops.embedding_bag_loop)
+    med_lit, n_lit, el_lit = timed(cpu_loops.baseline_loop)
+    return {"value": wl.num_bags / med_bag, "unit": "bags/s", "cores": threads, "kind": "port",
+            "sample": f"median of {n_bag} full passes ({el_bag:.1f} s) of the timed batch ({wl.num_bags} bags) "
+                      f"through F.embedding_bag per field (oracle/cpu_loops.py), {wl.table_dtype} tables in host "
+                      f"memory",
+            "baseline_loop": {"value": wl.num_bags / med_lit, "unit": "bags/s",
+                              "sample": f"median of {n_lit} passes ({el_lit:.1f} s) of the literal loop: clamp + "
+                                        "F.embedding + segment_reduce + cat (baseline/infer.py:256-263)"}}
 
 
 def bench_h2d(args, pkg, wls, dev):
@@ -269,6 +280,7 @@ def main():
     ap.add_argument("--long-threshold", type=int, default=0)
     ap.add_argument("--bins", action="store_true", help="run the device length-binning pass")
     ap.add_argument("--block-threshold", type=int, default=0)
+    ap.add_argument("--split-threshold", type=int, default=0)
     ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d"],
                     help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
                          "step end to end from host batches")
@@ -318,7 +330,8 @@ def main():
         pooled_tables = [pkg.quantize_embedding_int8(t) for t in tables]
     plan = pkg.PooledEmbedding(pooled_tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype,
                                long_threshold=args.long_threshold, use_bins=args.bins,
-                               block_threshold=args.block_threshold, max_batch=wl0.batch)
+                               block_threshold=args.block_threshold, max_batch=wl0.batch,
+                               split_threshold=args.split_threshold)
     out = torch.empty((wl0.batch, sum(wl0.dims)), dtype=wl0.out_dtype, device=dev)
     if args.stage == "layernorm":
         return bench_layernorm(args, pkg, plan, inputs, wl0, dev)

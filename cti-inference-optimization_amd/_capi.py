@@ -60,7 +60,8 @@ class Options(ctypes.Structure):
         ("long_threshold", ctypes.c_int32),
         ("use_bins", ctypes.c_int32),
         ("block_threshold", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 5),
+        ("split_threshold", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 4),
     ]
 
 

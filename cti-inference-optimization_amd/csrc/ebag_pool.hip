@@ -125,9 +125,10 @@ struct PoolParams {
   int64_t out_row_stride;   // elements
   int64_t batch;
   int64_t sub_threshold;    // longer bags are split over a wavefront's subgroups
-  int64_t block_threshold;  // longer bags go to the long kernel (kNoLimit without binning)
-  unsigned int* bin_count;  // binning: list length being built (NULL without binning)
-  unsigned int* bin_total;  // binning: list length handed to the long kernel
+  int64_t block_threshold;  // longer bags go to the list kernel (kNoLimit without binning)
+  int64_t split_threshold;  // listed bags longer than this are split over a workgroup
+  unsigned int* bin_count;  // binning: list lengths being built (NULL without binning): [0] one-wave, [2] split
+  unsigned int* bin_total;  // binning: list lengths handed to the list kernel: [0] one-wave, [2] split
   int32_t num_fields;
   int32_t num_tiles;
   int32_t tiles_per_field;  // every field of a launch has the same number of tiles
@@ -139,10 +140,16 @@ struct PoolParams {
 };
 
 // Workspace of the length-binning pass: counters, then the list of long bags.
+// Two lists share the workspace's entry array: bags pooled by one wavefront each grow from the
+// front, bags split over a workgroup's wavefronts grow from the back (together they never exceed
+// the number of bags of a launch, which the array holds).
 struct LongList {
-  unsigned int* count;  // list length, incremented by the binning pass
-  unsigned int* total;  // list length snapshot read by the long kernel
-  int64_t* bags;        // (local field index << 40) | sample index
+  unsigned int* count;   // one-wavefront list length, incremented by the binning pass
+  unsigned int* total;   // its snapshot read by the list kernel
+  unsigned int* count2;  // split list length
+  unsigned int* total2;
+  int64_t* bags;         // entries: (local field index << 40) | sample index
+  int64_t capacity;      // entries in `bags`; split entry j is bags[capacity - 1 - j]
 };
 constexpr int64_t kWorkspaceHeader = 256;
 
@@ -438,10 +445,13 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLds
 
 __device__ __forceinline__ void bin_handoff(const PoolParams& p) {
   if (p.bin_count && blockIdx.x == 0 && threadIdx.x == 0) {
-    // hand the finished list length to the long kernel and zero the counter for the next call
-    const unsigned int n = __hip_atomic_load(p.bin_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.bin_total, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p.bin_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // hand the finished list lengths to the list kernel and zero the counters for the next call
+#pragma unroll
+    for (int k = 0; k < 4; k += 2) {
+      const unsigned int n = __hip_atomic_load(p.bin_count + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.bin_total + k, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.bin_count + k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -453,29 +463,40 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
   pool_tile<TT, OT, LANES, VPL, BUF>(p, block_tile(), s);
 }
 
-// Length-binning pass: list the bags longer than block_threshold. grid (ceil(B/256), fields).
+// Length-binning pass: list the bags longer than block_threshold, those longer than
+// split_threshold on the split list. grid (ceil(B/256), fields).
 __global__ void __launch_bounds__(kBinThreads) bin_kernel(const PoolParams p, LongList l) {
   const int fi = static_cast<int>(blockIdx.y);
   const int64_t b = static_cast<int64_t>(blockIdx.x) * kBinThreads + threadIdx.x;
-  bool is_long = false;
+  bool one = false, split = false;
   if (b < p.batch) {
     int64_t s, e;
     bag_range(p, p.f[fi].gidx, b, s, e);
-    is_long = e - s > p.block_threshold;
+    split = e - s > p.split_threshold;
+    one = !split && e - s > p.block_threshold;
   }
-  const uint64_t m = __ballot(is_long);
-  if (m == 0) return;  // uniform over the wavefront
+  const uint64_t m1 = __ballot(one), m2 = __ballot(split);
+  if ((m1 | m2) == 0) return;  // uniform over the wavefront
   const int lane = lane_id();
-  unsigned int base = 0;
-  if (lane == 0) base = atomicAdd(l.count, static_cast<unsigned int>(__popcll(m)));
-  base = static_cast<unsigned int>(shfl_i32(static_cast<int>(base), 0));
-  if (is_long) {
-    const unsigned int pos = base + static_cast<unsigned int>(__popcll(m & ((1ull << lane) - 1ull)));
-    l.bags[pos] = (static_cast<int64_t>(fi) << 40) | b;
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int64_t entry = (static_cast<int64_t>(fi) << 40) | b;
+  if (m1) {
+    unsigned int base = 0;
+    if (lane == 0) base = atomicAdd(l.count, static_cast<unsigned int>(__popcll(m1)));
+    base = static_cast<unsigned int>(shfl_i32(static_cast<int>(base), 0));
+    if (one) l.bags[base + __popcll(m1 & below)] = entry;
+  }
+  if (m2) {
+    unsigned int base = 0;
+    if (lane == 0) base = atomicAdd(l.count2, static_cast<unsigned int>(__popcll(m2)));
+    base = static_cast<unsigned int>(shfl_i32(static_cast<int>(base), 0));
+    if (split) l.bags[l.capacity - 1 - (base + __popcll(m2 & below))] = entry;
   }
 }
 
-// Long kernel: LW wavefronts per workgroup; every listed bag is split into LW contiguous slices.
+// List kernel: LW wavefronts per workgroup. Every bag on the split list is cut into LW contiguous
+// slices, one per wavefront, combined through LDS in wavefront order; then every bag on the
+// one-wavefront list is pooled by one wavefront (lane groups take interleaved rows).
 template <typename TT, typename OT, int LANES, int VPL, int LW>
 __global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams p, LongList l) {
   using S = Shape<TT, LANES, VPL>;
@@ -484,9 +505,9 @@ __global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams 
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) >> 6;
   const int g = lane / LANES, sl = lane % LANES;
-  const unsigned int n = __hip_atomic_load(l.total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned int n = __hip_atomic_load(l.total2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (unsigned int j = blockIdx.x; j < n; j += gridDim.x) {
-    const int64_t item = l.bags[j];
+    const int64_t item = l.bags[l.capacity - 1 - j];
     const int fi = static_cast<int>(item >> 40);
     const int64_t b = item & ((int64_t{1} << 40) - 1);
     int64_t bs, be;
@@ -523,6 +544,21 @@ __global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams 
       store_bag<TT, OT, LANES, VPL>(p, b, p.f[fi].out_col, be - bs, r);
     }
     __syncthreads();
+  }
+  const unsigned int n1 = __hip_atomic_load(l.total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned int stride = gridDim.x * LW;
+  for (unsigned int j = blockIdx.x * LW + static_cast<unsigned int>(wave); j < n1; j += stride) {
+    const int64_t item = l.bags[j];
+    const int fi = static_cast<int>(item >> 40);
+    const int64_t b = item & ((int64_t{1} << 40) - 1);
+    int64_t bs, be;
+    bag_range(p, p.f[fi].gidx, b, bs, be);
+    float pa[S::NACC];
+#pragma unroll
+    for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
+    wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].row_scale, p.f[fi].max_row, p.f[fi].row_bytes, bs,
+                                       be, pa, s_ids + wave * kWave);
+    if (g == 0) store_bag<TT, OT, LANES, VPL>(p, b, p.f[fi].out_col, be - bs, pa);
   }
 }
 
@@ -605,6 +641,7 @@ int64_t default_sub_threshold(int variant) {
 
 // With binning, bags longer than this go to the long kernel.
 constexpr int64_t kDefaultBlockThreshold = 512;
+constexpr int64_t kDefaultSplitThreshold = 192;   // listed bags longer than this are split over a workgroup
 // Longest bag pooled by one subgroup (longer ones are split over the wavefront).
 constexpr int64_t kMaxShortBag = int64_t{1} << 24;
 
@@ -704,6 +741,7 @@ struct Job {
   int32_t sub_threshold;    // 0 = default, < 0 = split every non-empty bag
   int32_t use_bins;
   int32_t block_threshold;  // 0 = default (with bins)
+  int32_t split_threshold;  // 0 = default (with bins)
   void* workspace;
 };
 
@@ -724,6 +762,8 @@ int validate_tables(const Job& j) {
   return CTI_EBAG_OK;
 }
 
+int64_t workspace_bytes(int64_t batch, int32_t num_fields);
+
 int run_job(const Job& j, hipStream_t stream) {
   if (j.batch == 0 || j.num_fields == 0) return CTI_EBAG_OK;
   const int tb = dtype_bytes(j.tdt), ob = dtype_bytes(j.odt);
@@ -733,7 +773,10 @@ int run_job(const Job& j, hipStream_t stream) {
     char* ws = static_cast<char*>(j.workspace);
     list.count = reinterpret_cast<unsigned int*>(ws);
     list.total = reinterpret_cast<unsigned int*>(ws) + 1;
+    list.count2 = reinterpret_cast<unsigned int*>(ws) + 2;
+    list.total2 = reinterpret_cast<unsigned int*>(ws) + 3;
     list.bags = reinterpret_cast<int64_t*>(ws + kWorkspaceHeader);
+    list.capacity = (workspace_bytes(j.batch, j.num_fields) - kWorkspaceHeader) / 8;
   }
   // Group fields by kernel variant; each group is one launch sequence (per 64 fields).
   std::vector<int> var(j.num_fields);
@@ -760,6 +803,7 @@ int run_job(const Job& j, hipStream_t stream) {
       else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;
       const bool bins = j.use_bins && v != kVarGeneric;
       p.block_threshold = !bins ? kNoLimit : (j.block_threshold > 0 ? j.block_threshold : kDefaultBlockThreshold);
+      p.split_threshold = !bins ? kNoLimit : (j.split_threshold > 0 ? j.split_threshold : kDefaultSplitThreshold);
       // a bag is pooled by exactly one kernel: never call a listed (long) bag short
       if (v != kVarGeneric && p.sub_threshold > p.block_threshold) p.sub_threshold = p.block_threshold;
       // short-bag lengths are kept in 32 bits on the device
@@ -948,6 +992,7 @@ extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t 
     j.sub_threshold = opts->long_threshold;
     j.use_bins = opts->use_bins != 0;
     j.block_threshold = opts->block_threshold;
+    j.split_threshold = opts->split_threshold;
   }
   if (j.use_bins) {
     const int64_t need = workspace_bytes(batch_size, num_fields);

@@ -287,6 +287,7 @@ def embedding_bag_pooled(
     long_threshold: int = 0,
     use_bins: bool = False,
     block_threshold: int = 0,
+    split_threshold: int = 0,
 ) -> torch.Tensor:
     """Pool F fields with per-field tables into ``out[B, sum(D_f)]``.
 
@@ -302,7 +303,8 @@ def embedding_bag_pooled(
       long_threshold  bags longer than this are split over the lane groups of a wavefront
                (0 = per-shape default, -1 = split every non-empty bag).
       use_bins  run the device length-binning pass: bags longer than ``block_threshold``
-               (0 = default 512) are pooled by a kernel that splits each across the
+               (0 = default 512) are pooled by a second kernel: one wavefront per bag up to
+               ``split_threshold`` rows (0 = default 192), longer bags split across the
                wavefronts of a workgroup. A workspace is allocated for the call; use
                ``PooledEmbedding`` to keep one across calls.
     Equivalent to, per field, F.embedding_bag(clamp(values_f, 0, V_f-1), table_f, offsets_f,
@@ -333,6 +335,7 @@ def embedding_bag_pooled(
     opts.long_threshold = int(long_threshold)
     opts.use_bins = int(bool(use_bins))
     opts.block_threshold = int(block_threshold)
+    opts.split_threshold = int(split_threshold)
     lib = _capi.lib()
     ws, ws_bytes = None, 0
     if use_bins:
@@ -364,7 +367,8 @@ class PooledEmbedding:
 
     def __init__(self, tables: Sequence, pooling: str = "sum",
                  out_dtype: Optional[torch.dtype] = None, long_threshold: int = 0,
-                 use_bins: bool = False, block_threshold: int = 0, max_batch: int = 0):
+                 use_bins: bool = False, block_threshold: int = 0, max_batch: int = 0,
+                 split_threshold: int = 0):
         self.tables = list(tables)  # keeps the tensors (and int8 scales) alive
         self._descs, self.device, self._tdt, self.width, tdt = _table_descs(self.tables)
         self.num_fields = len(self.tables)
@@ -376,6 +380,7 @@ class PooledEmbedding:
         self._opts.long_threshold = int(long_threshold)
         self._opts.use_bins = int(bool(use_bins))
         self._opts.block_threshold = int(block_threshold)
+        self._opts.split_threshold = int(split_threshold)
         self._lib = _capi.lib()
         self._fn = self._lib.cti_ebag_forward
         self._ws, self._ws_bytes, self.max_batch = None, 0, int(max_batch)

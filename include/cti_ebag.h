@@ -84,15 +84,20 @@ typedef struct cti_ebag_table {
  *                    0 = default; a negative value splits every non-empty bag (used by tests).
  *   use_bins:        1 = run the device length-binning pass first: bags longer than
  *                    block_threshold are listed in the workspace and pooled by a second kernel
- *                    that splits each of them across the wavefronts of a workgroup (partials
- *                    combined through LDS in wavefront order). Needs the workspace.
+ *                    (one wavefront per bag, or, above split_threshold, the wavefronts of a
+ *                    workgroup with partials combined through LDS in wavefront order). Needs the
+ *                    workspace.
  *   block_threshold: with use_bins, the length above which a bag goes to that kernel
- *                    (0 = default, 512).                                                        */
+ *                    (0 = default, 512).
+ *   split_threshold: with use_bins, listed bags up to this length are pooled by one wavefront
+ *                    each (lane groups take interleaved rows); longer ones are split across the
+ *                    wavefronts of a workgroup (0 = default, 192).                             */
 typedef struct cti_ebag_options {
   int32_t long_threshold;
   int32_t use_bins;
   int32_t block_threshold;
-  int32_t reserved[5];
+  int32_t split_threshold;
+  int32_t reserved[4];
 } cti_ebag_options;
 
 /* ABI version this library was built with (CTI_EBAG_ABI_VERSION). */
@@ -131,9 +136,10 @@ int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* val_offsets,
  *   out           [B, out_row_stride] of `out_dtype`; field f writes columns
  *                 [out_col_f, out_col_f + dim_f)
  *   workspace     device scratch of at least cti_ebag_workspace_bytes(...) bytes, 256-byte
- *                 aligned, when opts->use_bins is set (else may be NULL). Its first 4 bytes (the
- *                 list counter) must be zero before the first use; every call leaves them zero
- *                 again, so one workspace serves any number of calls, one call at a time.
+ *                 aligned, when opts->use_bins is set (else may be NULL). Its first 16 bytes must
+ *                 be zero before the first use; every call leaves the two list counters in them
+ *                 (bytes 0-3 and 8-11) zero again, so one workspace serves any number of calls,
+ *                 one call at a time.
  *   opts          host pointer, may be NULL (all defaults)
  * Replaces the per-field loop at baseline/infer.py:256-263 and generalises the reference
  * kernel (online_best/infer.py:805-827) to per-field tables and mean pooling.

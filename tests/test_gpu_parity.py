@@ -40,12 +40,13 @@ def to_np(t, odt):
 
 
 def gpu_pool(pkg, dev, values, offsets, tables, tdt, pooling, odt, long_threshold=0, idx=torch.int64,
-             use_bins=False, block_threshold=0):
+             use_bins=False, block_threshold=0, split_threshold=0):
     v = torch.from_numpy(np.ascontiguousarray(values)).to(dev, idx)
     o = torch.from_numpy(np.ascontiguousarray(offsets)).to(dev)
     tt = [to_dev(t, tdt, dev) for t in tables]
     out = pkg.embedding_bag_pooled(v, o, tt, pooling=pooling, out_dtype=TORCH_DT[odt], long_threshold=long_threshold,
-                                   use_bins=use_bins, block_threshold=block_threshold)
+                                   use_bins=use_bins, block_threshold=block_threshold,
+                                   split_threshold=split_threshold)
     torch.cuda.synchronize()
     return to_np(out, odt)
 
@@ -154,13 +155,14 @@ def test_variant_split_within_bound(pkg, dev, dims, tdt, odt):
 @pytest.mark.parametrize("dims,tdt,odt", VARIANTS, ids=lambda x: str(x))
 @pytest.mark.parametrize("pooling", ["sum", "mean"])
 def test_variant_binned_long_kernel_within_bound(pkg, dev, dims, tdt, odt, pooling):
-    # bags longer than 40 are listed by the binning pass and split across 8 (or 4) wavefronts
+    # bags longer than 40 are listed by the binning pass: those up to split_threshold are pooled by
+    # one wavefront each, longer ones split across 8 (or 4) wavefronts
     case = random_case(900 + VARIANTS.index((dims, tdt, odt)), F=3, B=41, dims=dims, V=(500,), tdt=tdt,
                        max_len=60, long_every=4, long_len=900)
     ref64, bound = f64_pool(case.values, case.offsets, case.tables, tdt, pooling, case.B)
-    for thr in (0, 8):
+    for thr, split in ((0, 0), (8, 0), (0, 50), (0, 100000)):
         got = gpu_pool(pkg, dev, case.values, case.offsets, case.tables, tdt, pooling, odt, long_threshold=thr,
-                       use_bins=True, block_threshold=40)
+                       use_bins=True, block_threshold=40, split_threshold=split)
         assert_within_bound(got, odt, ref64, bound)
     # the short bags never reach a split path: bit for bit with the oracle
     want = orc.pool_c(case.values, case.offsets, case.tables, tdt, pooling, odt)
@@ -180,23 +182,26 @@ def test_integer_tables_bitwise_in_every_path(pkg, dev):
     for thr in (NO_SPLIT, ALL_SPLIT, 0, 40):
         got = gpu_pool(pkg, dev, case.values, case.offsets, case.tables, "bf16", "sum", "f32", long_threshold=thr)
         assert np.array_equal(got, want), thr
-    for bt in (0, 1, 100):
+    for bt, split in ((0, 0), (1, 0), (100, 0), (1, 60), (20, 1000), (20, 2000)):
         got = gpu_pool(pkg, dev, case.values, case.offsets, case.tables, "bf16", "sum", "f32", use_bins=True,
-                       block_threshold=bt)
-        assert np.array_equal(got, want), bt
+                       block_threshold=bt, split_threshold=split)
+        assert np.array_equal(got, want), (bt, split)
 
 
 def test_binning_workspace_is_left_zeroed(pkg, dev):
     case = random_case(77, F=4, B=300, dims=(128,), V=(900,), tdt="bf16", max_len=30, long_every=7, long_len=600)
     tt = [to_dev(t, "bf16", dev) for t in case.tables]
-    plan = pkg.PooledEmbedding(tt, pooling="sum", use_bins=True, block_threshold=50, max_batch=case.B)
+    plan = pkg.PooledEmbedding(tt, pooling="sum", use_bins=True, block_threshold=50, max_batch=case.B,
+                               split_threshold=300)
     v = torch.from_numpy(case.values).to(dev)
     o = torch.from_numpy(case.offsets).to(dev)
     first = plan(v, o).clone()
     for _ in range(3):
         again = plan(v, o)
     torch.cuda.synchronize()
-    assert torch.count_nonzero(plan._ws[:4]).item() == 0  # the list counter is back at zero
+    # the two list counters (bytes 0-3 and 8-11) are back at zero; bytes 4-7 and 12-15 hold the
+    # list lengths the last call handed to the list kernel
+    assert torch.count_nonzero(plan._ws[0:4]).item() == 0 and torch.count_nonzero(plan._ws[8:12]).item() == 0
     assert torch.equal(first.view(torch.int16), again.view(torch.int16))
     ref64, bound = f64_pool(case.values, case.offsets, case.tables, "bf16", "sum", case.B)
     assert_within_bound(to_np(again, "bf16"), "bf16", ref64, bound)
