@@ -464,8 +464,12 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
 }
 
 // Length-binning pass: list the bags longer than block_threshold, those longer than
-// split_threshold on the split list. grid (ceil(B/256), fields).
+// split_threshold on the split list. grid (ceil(B/256), fields). The workgroup's wavefronts
+// combine their counts in LDS, so each list costs one global atomic per workgroup.
 __global__ void __launch_bounds__(kBinThreads) bin_kernel(const PoolParams p, LongList l) {
+  constexpr int kWaves = kBinThreads / kWave;
+  __shared__ unsigned int s_cnt[2][kWaves];
+  __shared__ unsigned int s_base[2];
   const int fi = static_cast<int>(blockIdx.y);
   const int64_t b = static_cast<int64_t>(blockIdx.x) * kBinThreads + threadIdx.x;
   bool one = false, split = false;
@@ -475,23 +479,30 @@ __global__ void __launch_bounds__(kBinThreads) bin_kernel(const PoolParams p, Lo
     split = e - s > p.split_threshold;
     one = !split && e - s > p.block_threshold;
   }
-  const uint64_t m1 = __ballot(one), m2 = __ballot(split);
-  if ((m1 | m2) == 0) return;  // uniform over the wavefront
   const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const uint64_t m1 = __ballot(one), m2 = __ballot(split);
+  if (lane == 0) {
+    s_cnt[0][wave] = static_cast<unsigned int>(__popcll(m1));
+    s_cnt[1][wave] = static_cast<unsigned int>(__popcll(m2));
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    unsigned int n = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) n += s_cnt[threadIdx.x][w];
+    s_base[threadIdx.x] = n ? atomicAdd(threadIdx.x == 0 ? l.count : l.count2, n) : 0u;
+  }
+  __syncthreads();
+  unsigned int before1 = 0, before2 = 0;  // entries of the lower wavefronts of this workgroup
+  for (int w = 0; w < wave; ++w) {
+    before1 += s_cnt[0][w];
+    before2 += s_cnt[1][w];
+  }
   const uint64_t below = (1ull << lane) - 1ull;
   const int64_t entry = (static_cast<int64_t>(fi) << 40) | b;
-  if (m1) {
-    unsigned int base = 0;
-    if (lane == 0) base = atomicAdd(l.count, static_cast<unsigned int>(__popcll(m1)));
-    base = static_cast<unsigned int>(shfl_i32(static_cast<int>(base), 0));
-    if (one) l.bags[base + __popcll(m1 & below)] = entry;
-  }
-  if (m2) {
-    unsigned int base = 0;
-    if (lane == 0) base = atomicAdd(l.count2, static_cast<unsigned int>(__popcll(m2)));
-    base = static_cast<unsigned int>(shfl_i32(static_cast<int>(base), 0));
-    if (split) l.bags[l.capacity - 1 - (base + __popcll(m2 & below))] = entry;
-  }
+  if (one) l.bags[s_base[0] + before1 + __popcll(m1 & below)] = entry;
+  if (split) l.bags[l.capacity - 1 - (s_base[1] + before2 + __popcll(m2 & below))] = entry;
 }
 
 // List kernel: LW wavefronts per workgroup. Every bag on the split list is cut into LW contiguous
