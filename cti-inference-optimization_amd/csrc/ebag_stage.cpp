@@ -11,12 +11,14 @@
 // converted into one contiguous pinned region, which one hipMemcpyAsync sends to the device.
 #include <stdint.h>
 
+#include <pthread.h>
 #include <string.h>
 
 #include <algorithm>
 #include <atomic>
 #include <condition_variable>
 #include <mutex>
+#include <new>
 #include <thread>
 #include <vector>
 
@@ -83,11 +85,21 @@ struct Job {
 // no worker is inside work() (busy_ == 0, checked under m_), and run() returns only when every
 // chunk is done and no worker is busy, so a worker that wakes late finds either the job it was
 // woken for (with nothing left to claim) or the next one, never a mix. The pool is never
-// destroyed: its threads end with the process.
+// destroyed: its threads end with the process; a forked child starts a new pool.
 class Pool {
  public:
   static Pool& get() {
-    static Pool* pool = new Pool();
+    static std::once_flag registered;
+    std::call_once(registered, [] { pthread_atfork(nullptr, nullptr, &Pool::forget_in_child); });
+    Pool* pool = instance().load(std::memory_order_acquire);
+    if (!pool) {
+      std::lock_guard<std::mutex> lk(create_mutex());
+      pool = instance().load(std::memory_order_relaxed);
+      if (!pool) {
+        pool = new Pool();
+        instance().store(pool, std::memory_order_release);
+      }
+    }
     return *pool;
   }
 
@@ -114,6 +126,21 @@ class Pool {
   }
 
  private:
+  static std::atomic<Pool*>& instance() {
+    static std::atomic<Pool*> p{nullptr};
+    return p;
+  }
+  static std::mutex& create_mutex() {
+    static std::mutex m;
+    return m;
+  }
+  // A forked child has none of the parent's worker threads and may inherit a mutex locked by a
+  // job that was running in another thread: it starts a pool of its own (the old one is leaked).
+  static void forget_in_child() {
+    instance().store(nullptr, std::memory_order_relaxed);
+    new (&create_mutex()) std::mutex();
+  }
+
   // Claim chunks until none are left; returns how many this thread completed.
   int64_t work() {
     int64_t done = 0;

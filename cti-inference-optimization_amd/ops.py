@@ -127,9 +127,13 @@ def _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev):
     return _capi.index_code(flat_values.dtype), _capi.index_code(flat_row_offsets.dtype)
 
 
-def _same_offset_type(val_offsets: torch.Tensor, flat_row_offsets: torch.Tensor) -> torch.Tensor:
+def _same_offset_type(val_offsets: torch.Tensor, flat_row_offsets: torch.Tensor, nnz: int) -> torch.Tensor:
     """val_offsets in flat_row_offsets' dtype (the reference widens only val_offsets, :747)."""
-    return val_offsets if val_offsets.dtype == flat_row_offsets.dtype else val_offsets.to(flat_row_offsets.dtype)
+    if val_offsets.dtype == flat_row_offsets.dtype:
+        return val_offsets
+    if flat_row_offsets.dtype == torch.int32 and nnz >= 2 ** 31:
+        raise ValueError("int32 row offsets cannot address a batch of 2^31 or more ids")
+    return val_offsets.to(flat_row_offsets.dtype)
 
 
 def fused_all_slots_embedding_int8(
@@ -155,7 +159,7 @@ def fused_all_slots_embedding_int8(
     dev = weight_int8.device
     _require_device_tensor("weight_int8", weight_int8)
     icode, ocode = _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
-    val_offsets = _same_offset_type(val_offsets, flat_row_offsets)
+    val_offsets = _same_offset_type(val_offsets, flat_row_offsets, flat_values.numel())
     _require_device_tensor("scale", scale, dev)
     _require_contiguous("weight_int8", weight_int8)
     _require_contiguous("scale", scale)
@@ -219,7 +223,7 @@ def fused_all_slots_embedding(
     dev = weight.device
     _require_device_tensor("weight", weight)
     icode, ocode = _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
-    val_offsets = _same_offset_type(val_offsets, flat_row_offsets)
+    val_offsets = _same_offset_type(val_offsets, flat_row_offsets, flat_values.numel())
     if weight.dim() != 2:
         raise ValueError(f"weight must be 2-D [V, D], got shape {tuple(weight.shape)}")
     _require_contiguous("weight", weight)

@@ -39,8 +39,9 @@ class InputStager:
     """Ring of pinned host / device regions for flat-layout batches.
 
     ``max_nnz``, ``num_slots`` and ``max_batch`` size the regions; ``compact`` selects int32 ids
-    and offsets (else int64, as the reference sends them). Synchronise the device before dropping
-    a stager whose copies or consumers may still be running.
+    and offsets (else int64, as the reference sends them). Dropping the stager (or ``close()``)
+    waits for its copies; work that still reads a staged batch must be ordered before any reuse of
+    that memory by the caller.
     """
 
     def __init__(self, max_nnz: int, num_slots: int, max_batch: int, device=None, depth: int = 2,
@@ -119,6 +120,18 @@ class InputStager:
             off = self._offset(counts, part)
             out[k] = d[off:off + c * (4 if self.compact else 8)].view(self.dtype)
         return out
+
+    def close(self) -> None:
+        """Wait for this stager's copies: its pinned regions are then safe to free. (The copies are
+        issued by the library, so torch's pinned-memory allocator does not track them.)"""
+        if getattr(self, "copy_stream", None) is not None:
+            self.copy_stream.synchronize()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the HIP runtime may already be gone
+            pass
 
     def release(self, staged: dict) -> None:
         """Mark the staged batch's device region reusable once the work enqueued so far on torch's

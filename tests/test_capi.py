@@ -280,3 +280,24 @@ def test_stage_copy_rejects_bad_arguments(pkg):
     assert f(src, bad, cnt, 2, c.I32, 64, 1 << 20, 64, 4, None) == c.EINVAL
     zero = (ctypes.c_int64 * 2)(0, 0)
     assert f(src, st, zero, 2, c.I32, None, 0, None, 4, None) == c.OK
+
+
+def test_narrow_ids_in_a_forked_child(pkg):
+    """The host pool is rebuilt in a forked child (DataLoader workers fork)."""
+    import numpy as np
+
+    lib = pkg._capi.lib()
+    src = np.arange(-(1 << 19), 1 << 19, dtype=np.int64) * (1 << 20)
+    dst = np.zeros(src.size, np.int32)
+    assert lib.cti_ebag_narrow_ids(src.ctypes.data, src.size, dst.ctypes.data, 8) == 0
+    pid = os.fork()
+    if pid == 0:
+        code = 1
+        try:
+            d2 = np.zeros(src.size, np.int32)
+            ok = lib.cti_ebag_narrow_ids(src.ctypes.data, src.size, d2.ctypes.data, 8) == 0
+            code = 0 if ok and np.array_equal(d2, np.clip(src, -(2 ** 31), 2 ** 31 - 1).astype(np.int32)) else 1
+        finally:
+            os._exit(code)
+    _, status = os.waitpid(pid, 0)
+    assert os.WIFEXITED(status) and os.WEXITSTATUS(status) == 0
