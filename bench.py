@@ -17,6 +17,11 @@ leaves them) to the GPU and pools it with the reference launch (one shared table
 with int64 inputs, (c) the same with ids and offsets narrowed to int32 on the host. The line
 reports bags/s per variant, the copy-only and pool-only times, and the bytes moved per batch.
 
+`--stage encoder` times the encoder's front end on the workload's batches (reference layout, one
+shared table as in the reference, sum pooling): the pooling kernel followed by the LayerNorm
+kernel, against the fused kernel that normalises each pooled row on chip
+(online_best/infer.py:1050-1076).
+
 `--stage layernorm` times the encoder's input LayerNorm instead (online_best/infer.py:1061-1076):
 the workload's batches are pooled once, and each step normalises one pooled block
 [B, sum(D)] (rows/s; roofline bytes = the block read and written plus gamma and beta).
@@ -58,10 +63,10 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def traffic_from_profiles(workload):
+def traffic_from_profiles(workload, kernel="pool_kernel"):
     """HBM bytes per launch recorded by the rocprofv3 counter runs, read from the line
-    `hbm_bytes_per_launch: N` of profiles/pool_kernel_<workload>.md, or None."""
-    path = os.path.join(ROOT, "profiles", f"pool_kernel_{workload}.md")
+    `hbm_bytes_per_launch: N` of profiles/<kernel>_<workload>.md, or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}.md")
     if not os.path.exists(path):
         return None
     with open(path) as fh:
@@ -224,6 +229,85 @@ def bench_h2d(args, pkg, wls, dev):
     print(json.dumps(rec), flush=True)
 
 
+def bench_encoder(args, pkg, wls, dev):
+    """Pooling + input LayerNorm: two kernels against the fused kernel (reference layout)."""
+    import numpy as np
+    import torch
+
+    wl0 = wls[0]
+    F, B, D = wl0.num_fields, wl0.batch, wl0.dims[0]
+    V = max(wl0.vocab)
+    batches = []
+    for wl in wls:
+        off = wl.offsets
+        ro = np.stack([off[f * B:(f + 1) * B + 1] - off[f * B] for f in range(F)]).reshape(-1)
+        batches.append((torch.from_numpy(wl.values).to(dev), torch.from_numpy(off[0:F * B:B].copy()).to(dev),
+                        torch.from_numpy(ro).to(dev)))
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    weight = torch.empty((V, D), dtype=wl0.table_dtype, device=dev)
+    weight.normal_(0.0, 0.01, generator=g)
+    gamma = torch.empty(F * D, dtype=wl0.table_dtype, device=dev).normal_(1.0, 0.1, generator=g)
+    beta = torch.empty(F * D, dtype=wl0.table_dtype, device=dev).normal_(0.0, 0.1, generator=g)
+    out = torch.empty((B, F * D), dtype=wl0.table_dtype, device=dev)
+    n = len(batches)
+
+    def separate(i):
+        v, vo, ro = batches[i % n]
+        pkg.fused_all_slots_embedding(v, vo, ro, weight, out, B, D, V - 1)
+        pkg.layer_norm(out, gamma, beta, 1e-5, out=out)
+
+    def fused(i):
+        v, vo, ro = batches[i % n]
+        pkg.fused_all_slots_embedding_layernorm(v, vo, ro, weight, out, B, D, V - 1, gamma, beta, 1e-5)
+
+    def timed(step):
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            step(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps / 1e3
+
+    log("pooling then LayerNorm")
+    t_sep = timed(separate)
+    log("fused")
+    t_fused = timed(fused)
+    # the pooling's algorithmic bytes with the reference layout's offsets (row offsets + slot bases)
+    pool_bytes = float(np.mean([wl.bytes_algorithmic() - wl.offsets.size * 8 + (F * (B + 1) + F) * 8 for wl in wls]))
+    fused_bytes = pool_bytes + 2 * F * D * 2  # + gamma and beta
+    achieved = fused_bytes / t_fused / 1e9
+    rec = {
+        "metric": "pooled and normalised rows/sec (encoder front end), B=4096x28 fields, D=128 bf16",
+        "value": B / t_fused,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": t_fused * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": f"synthetic: {n} seeded index sets rotated, one shared N(0, 0.01) table [{V}, {D}], "
+                "gamma ~ N(1, 0.1), beta ~ N(0, 0.1)",
+        "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}; reference layout, one shared "
+                               "table, sum pooling, then LayerNorm over [B, 28*128]"},
+        "us_per_step": {"pool_then_layernorm": t_sep * 1e6, "fused": t_fused * 1e6},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic_from_profiles(args.workload + "-shared", "pool_norm_kernel"),
+                     "kernel": "pool_norm_kernel",
+                     "bytes_per_launch": fused_bytes, "launch_us_mean": t_fused * 1e6},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def bench_layernorm(args, pkg, plan, inputs, wl0, dev):
     """Time the input LayerNorm over pooled blocks of the workload (one block per step, rotated)."""
     import torch
@@ -281,7 +365,7 @@ def main():
     ap.add_argument("--bins", action="store_true", help="run the device length-binning pass")
     ap.add_argument("--block-threshold", type=int, default=0)
     ap.add_argument("--split-threshold", type=int, default=0)
-    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d"],
+    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d", "encoder"],
                     help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
                          "step end to end from host batches")
     ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
@@ -321,6 +405,8 @@ def main():
     wl0 = wls[0]
     if args.stage == "h2d":
         return bench_h2d(args, pkg, wls, dev)
+    if args.stage == "encoder":
+        return bench_encoder(args, pkg, wls, dev)
     log("filling tables on the device")
     tables = W.make_tables(wl0, dev, seed=0)
     inputs = [W.to_device(wl, dev) for wl in wls]

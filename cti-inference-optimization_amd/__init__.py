@@ -3,6 +3,7 @@
 Public surface:
   fused_all_slots_embedding  drop-in for the reference's fused_all_slots_embedding_kernel launch
   fused_embedding            the RepEncoder.forward fused step on a flat-layout batch dict
+  fused_all_slots_embedding_layernorm   the fused step with the input LayerNorm in one kernel
   quantize_embedding_int8    int8 row quantisation of a table (int8 rows + fp32 row scales)
   fused_all_slots_embedding_int8   drop-in for the reference's int8 fused kernel launch
   embedding_bag_pooled       per-field tables, global offsets, sum/mean, chosen output dtype
@@ -20,7 +21,7 @@ from .encoder import RepEncoder
 from .layout import collate_flat_layout, merge_batches, pack_slots, prebuild_flat_layout
 from .staging import InputStager, move_model_inputs_to_device
 from .ops import (PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_all_slots_embedding_int8,
-                  fused_embedding, layer_norm, quantize_embedding_int8)
+                  fused_all_slots_embedding_layernorm, fused_embedding, layer_norm, quantize_embedding_int8)
 
 __all__ = [
     "EbagError",
@@ -37,6 +38,7 @@ __all__ = [
     "fused_all_slots_embedding",
     "fused_embedding",
     "fused_all_slots_embedding_int8",
+    "fused_all_slots_embedding_layernorm",
     "quantize_embedding_int8",
     "layer_norm",
     "workloads",

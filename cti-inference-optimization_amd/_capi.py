@@ -100,6 +100,10 @@ SIGNATURES = {
     ),
     "cti_ebag_quantize_int8": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _P, _P, _P]),
     "cti_ebag_narrow_ids": (ctypes.c_int, [_P, _I64, _P, _I32]),
+    "cti_ebag_fused_all_slots_layernorm": (
+        ctypes.c_int,
+        [_P, _I32, _P, _P, _I32, _P, _I32, _P, _I64, _I32, _I32, _I64, _I64, _I32, _P, _P, _I32, ctypes.c_float, _P],
+    ),
     "cti_ebag_stage_copy": (
         ctypes.c_int,
         [_PP, ctypes.POINTER(ctypes.c_int32), _PI64, _I32, _I32, _P, _I64, _P, _I32, _P],

@@ -252,4 +252,65 @@ __device__ __forceinline__ int64_t clamp_i64(int64_t v, int64_t lo, int64_t hi) 
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
+
+// Sum over the workgroup (WAVES wavefronts) in a fixed order: xor butterfly inside each
+// wavefront, then the wavefront sums in wavefront order. Every thread gets the total.
+template <int WAVES>
+__device__ __forceinline__ float block_sum(float v, float* s_red) {
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) v += shfl_xor_f32(v, m);
+  if constexpr (WAVES == 1) {
+    return v;
+  } else {
+    const int w = static_cast<int>(threadIdx.x) / kWave;
+    __syncthreads();  // earlier readers of s_red are done
+    if (lane_id() == 0) s_red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < WAVES; ++i) t += s_red[i];
+    return t;
+  }
+}
+
+__device__ __forceinline__ void unpack16(const uint4& v, float* a, float) {
+  a[0] = __uint_as_float(v.x);
+  a[1] = __uint_as_float(v.y);
+  a[2] = __uint_as_float(v.z);
+  a[3] = __uint_as_float(v.w);
+}
+__device__ __forceinline__ void unpack16(const uint4& v, float* a, bf16_t) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[2 * i] = __uint_as_float(w[i] << 16);
+    a[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void unpack16(const uint4& v, float* a, f16_t) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+    a[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+  }
+}
+
+// VEC parameters starting at element c0 (16-byte aligned): 16-byte loads, or one 8-byte load.
+template <typename PT, int VEC>
+__device__ __forceinline__ void load_params(const void* p, int64_t c0, float* out) {
+  const char* base = static_cast<const char*>(p) + c0 * Elem<PT>::kBytes;
+  constexpr int BYTES = VEC * Elem<PT>::kBytes;
+  if constexpr (BYTES == 8) {  // four 16-bit parameters
+    const uint2 u = *reinterpret_cast<const uint2*>(base);
+    float t[8];
+    unpack16(make_uint4(u.x, u.y, 0u, 0u), t, PT{});
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) out[e] = t[e];
+  } else {
+#pragma unroll
+    for (int h = 0; h < BYTES / 16; ++h) unpack16(load16(base + h * 16), out + h * (16 / Elem<PT>::kBytes), PT{});
+  }
+}
+
 }  // namespace cti

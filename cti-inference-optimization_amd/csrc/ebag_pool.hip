@@ -463,6 +463,198 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
   pool_tile<TT, OT, LANES, VPL, BUF>(p, block_tile(), s);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Pooling with the input LayerNorm fused into the writer (online_best/infer.py:1050-1076): one
+// workgroup owns whole output rows, so the pooled row never goes to HBM before normalisation.
+// One shared table (the reference's single nn.Embedding), uniform row width, one row vector per
+// lane. Wavefront w pools fields w, w + W, ... of its sample exactly as the main kernel pools a
+// tile (length-ranked rounds, one lane group per short bag in element order, the whole
+// wavefront for longer bags) and writes each result, rounded to the output type, into an LDS
+// copy of the row; the workgroup then normalises that row (fp32 mean and variance, fixed
+// reduction order) and stores it once.
+constexpr int kFusedWaves = 4;
+constexpr int kFusedBagsPerWave = 32;  // samples per workgroup * ceil(fields / kFusedWaves) <= 32
+
+struct FusedLds {  // one per wavefront
+  unsigned int ids[kWave];
+  int order[kFusedBagsPerWave];
+  int len[kFusedBagsPerWave];
+  int64_t start[kFusedBagsPerWave];
+};
+
+struct FusedNorm {
+  const void* gamma;
+  const void* beta;
+  float eps;
+};
+
+// Orders this wavefront's LDS accesses (its lanes exchange row ids through LDS); the four
+// wavefronts of a fused workgroup pool independently, so no workgroup barrier is used here.
+__device__ __forceinline__ void wave_sync() { __builtin_amdgcn_wave_barrier(); }
+
+template <typename TT, typename PT, int LANES, int SPW, bool BUF>
+__global__ void __launch_bounds__(kFusedWaves * kWave) pool_norm_kernel(const PoolParams p, const FusedNorm fn) {
+  using S = Shape<TT, LANES, 1>;
+  constexpr int U = S::U;
+  constexpr int R = S::R;
+  constexpr int W = kFusedWaves;
+  extern __shared__ uint4 s_row_raw[];  // the output rows: SPW * F * D elements of TT
+  __shared__ FusedLds s_w[W];
+  __shared__ float s_red[W];
+  TT* const row = reinterpret_cast<TT*>(s_row_raw);
+
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int g = lane / LANES, sl = lane % LANES;
+  const int64_t b0 = static_cast<int64_t>(block_tile()) * SPW;  // XCD x pools a contiguous sample range
+  const int F = p.num_fields;
+  const int D = p.f[0].dim;
+  const char* const table = p.f[0].table;
+  const int64_t max_row = p.f[0].max_row;
+  const int64_t row_bytes = p.f[0].row_bytes;
+  const Rsrc rsrc = make_rsrc(table, BUF ? p.f[0].span_bytes : 0u);
+  const unsigned int shift = static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(row_bytes)));
+  const unsigned int r_pad = BUF ? 0xffffffffu >> shift : 0u;
+  FusedLds& s = s_w[wave];
+
+  // Lane i describes this wavefront's bag i: field wave + W * (i % nk) of sample b0 + i / nk.
+  // Row position of bag i in the LDS rows: (i / nk) * F + field.
+  const int nk = wave < F ? (F - wave + W - 1) / W : 0;
+  auto bag_pos = [&](int i) { return (i / nk) * F + wave + W * (i % nk); };
+  bool valid = lane < SPW * nk;
+  int64_t start = 0, end = 0;
+  if (valid) {
+    const int64_t bb = b0 + lane / nk;
+    valid = bb < p.batch;
+    if (valid) bag_range(p, p.f[wave + W * (lane % nk)].gidx, bb, start, end);
+  }
+  const int64_t L = end - start;
+  const bool shortb = valid && L <= p.sub_threshold;
+  const bool medium = valid && L > p.sub_threshold;
+  const int n_short = __popcll(__ballot(shortb));
+  const int key = shortb ? static_cast<int>(L) : -1;
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < kFusedBagsPerWave; ++j) {
+    const int kj = __builtin_amdgcn_readlane(key, j);
+    rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
+  }
+  if (shortb) {
+    s.order[rank] = lane;
+    s.len[lane] = static_cast<int>(L);
+    s.start[lane] = start;
+  }
+  wave_sync();
+
+  auto write_row = [&](int bag, int64_t Lb, float* a) {
+    float r[S::NACC];
+#pragma unroll
+    for (int i = 0; i < S::NACC; ++i) r[i] = a[i];
+    if (p.pooling == CTI_EBAG_MEAN && Lb > 0)
+      div_by_count<S::NACC>(r, 1.0 / static_cast<double>(Lb), static_cast<float>(Lb));
+    store_out<S::VEC>(row + static_cast<int64_t>(bag_pos(bag)) * D + sl * S::VEC, r);
+  };
+
+  for (int r0 = 0; r0 < n_short; r0 += R) {
+    const int slot = r0 + g;
+    const bool has = slot < n_short;
+    const int bi = has ? s.order[slot] : 0;
+    const int Lb = has ? s.len[bi] : 0;
+    const int64_t bs = has ? s.start[bi] : 0;
+    float acc[S::NACC];
+#pragma unroll
+    for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
+    for (int c = 0; __ballot(c < Lb) != 0; c += LANES) {
+      wave_sync();  // this chunk's LDS writes come after the last chunk's reads
+      s.ids[lane] = c + sl < Lb ? static_cast<unsigned int>(clamp_i64(load_index(p, bs + c + sl), 0, max_row)) : r_pad;
+      wave_sync();
+      const int live = Lb - c < LANES ? Lb - c : LANES;
+      for (int k = 0; k < LANES; k += U) {
+        if (__ballot(k < live) == 0) break;
+        uint4 v[U][1];
+        float sc[U];
+        if constexpr (BUF) {
+          unsigned int r[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) r[u] = s.ids[g * LANES + k + u];
+          const unsigned int lane_off = static_cast<unsigned int>(sl * S::VB);
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            v[u][0] = buffer_load_vec<TT>(rsrc, (r[u] << shift) + lane_off);
+            sc[u] = 1.f;
+          }
+          __builtin_amdgcn_sched_barrier(0);  // issue every load of the step before consuming any
+        } else {
+          load_step<TT, LANES, 1>(table, nullptr, row_bytes, s.ids + g * LANES, sl, k, live, v, sc);
+        }
+        add_step<TT, LANES, 1>(acc, v, sc);
+      }
+    }
+    if (has) write_row(bi, Lb, acc);
+  }
+  for (uint64_t m = __ballot(medium); m;) {
+    const int src = __ffsll(static_cast<long long>(m)) - 1;  // the bag's lane
+    m &= m - 1;
+    const int64_t bs = shfl_i64(start, src), be = shfl_i64(end, src);
+    float pa[S::NACC];
+#pragma unroll
+    for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
+    wave_sync();
+    wave_slice_partial<TT, LANES, 1>(p, table, nullptr, max_row, row_bytes, bs, be, pa, s.ids);
+    if (g == 0) write_row(src, be - bs, pa);
+  }
+  __syncthreads();  // the whole rows are in LDS
+
+  // LayerNorm of each row (online_best/infer.py:843-856): fp32 mean, fp32 variance of the
+  // deviations, y = (x - mean) * rstd * gamma + beta rounded once to the output type. The rows
+  // of the workgroup's samples share each gamma / beta load.
+  constexpr int VEC = 16 / Elem<TT>::kBytes;
+  const int cols = F * D;
+  const int nvec = cols / VEC;
+  const int t = static_cast<int>(threadIdx.x);
+  constexpr int THREADS = W * kWave;
+  const char* const rb = reinterpret_cast<const char*>(row);
+  const int64_t rstride = static_cast<int64_t>(cols) * Elem<TT>::kBytes;
+  const float n = static_cast<float>(cols);
+  float mean[SPW], rstd[SPW];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    float sum = 0.f;
+    for (int i = t; i < nvec; i += THREADS) {
+      float x[VEC];
+      unpack16(load16(rb + j * rstride + i * 16), x, TT{});
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += x[e];
+    }
+    mean[j] = block_sum<W>(sum, s_red) / n;
+    float q = 0.f;
+    for (int i = t; i < nvec; i += THREADS) {
+      float x[VEC];
+      unpack16(load16(rb + j * rstride + i * 16), x, TT{});
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float d = x[e] - mean[j];
+        q += d * d;
+      }
+    }
+    rstd[j] = 1.0f / __builtin_sqrtf(block_sum<W>(q, s_red) / n + fn.eps);
+  }
+  for (int i = t; i < nvec; i += THREADS) {
+    float gm[VEC], bt[VEC];
+    load_params<PT, VEC>(fn.gamma, static_cast<int64_t>(i) * VEC, gm);
+    load_params<PT, VEC>(fn.beta, static_cast<int64_t>(i) * VEC, bt);
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      if (b0 + j >= p.batch) break;
+      float x[VEC], r[VEC];
+      unpack16(load16(rb + j * rstride + i * 16), x, TT{});
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) r[e] = (x[e] - mean[j]) * rstd[j] * gm[e] + bt[e];
+      store_out<VEC>(reinterpret_cast<TT*>(p.out) + (b0 + j) * p.out_row_stride + static_cast<int64_t>(i) * VEC, r);
+    }
+  }
+}
+
 // Length-binning pass: list the bags longer than block_threshold, those longer than
 // split_threshold on the split list. grid (ceil(B/256), fields). The workgroup's wavefronts
 // combine their counts in LDS, so each list costs one global atomic per workgroup.
@@ -921,6 +1113,146 @@ int run_all_slots(const void* values, int32_t index_type, const void* val_offset
 
 }  // namespace
 }  // namespace cti
+
+namespace cti {
+namespace {
+
+template <typename TT, typename PT, int LANES>
+hipError_t launch_fused(const PoolParams& p, const FusedNorm& fn, int spw, size_t row_lds, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((p.batch + spw - 1) / spw)), block(kFusedWaves * kWave);
+  const size_t lds = row_lds * spw;
+  switch (spw * 2 + (p.buffer_ok ? 1 : 0)) {
+    case 2: hipLaunchKernelGGL((pool_norm_kernel<TT, PT, LANES, 1, false>), grid, block, lds, s, p, fn); break;
+    case 3: hipLaunchKernelGGL((pool_norm_kernel<TT, PT, LANES, 1, true>), grid, block, lds, s, p, fn); break;
+    case 4: hipLaunchKernelGGL((pool_norm_kernel<TT, PT, LANES, 2, false>), grid, block, lds, s, p, fn); break;
+    case 5: hipLaunchKernelGGL((pool_norm_kernel<TT, PT, LANES, 2, true>), grid, block, lds, s, p, fn); break;
+    case 8: hipLaunchKernelGGL((pool_norm_kernel<TT, PT, LANES, 4, false>), grid, block, lds, s, p, fn); break;
+    default: hipLaunchKernelGGL((pool_norm_kernel<TT, PT, LANES, 4, true>), grid, block, lds, s, p, fn); break;
+  }
+  return hipGetLastError();
+}
+
+template <typename TT, typename PT>
+hipError_t launch_fused_lanes(int lanes, const PoolParams& p, const FusedNorm& fn, int spw, size_t row_lds,
+                              hipStream_t s) {
+  switch (lanes) {
+    case 4: return launch_fused<TT, PT, 4>(p, fn, spw, row_lds, s);
+    case 8: return launch_fused<TT, PT, 8>(p, fn, spw, row_lds, s);
+    case 16: return launch_fused<TT, PT, 16>(p, fn, spw, row_lds, s);
+    case 32: return launch_fused<TT, PT, 32>(p, fn, spw, row_lds, s);
+    default: return launch_fused<TT, PT, 64>(p, fn, spw, row_lds, s);
+  }
+}
+
+#ifndef CTI_EBAG_FUSED_SAMPLES
+#define CTI_EBAG_FUSED_SAMPLES 2
+#endif
+
+// Samples per fused workgroup: up to CTI_EBAG_FUSED_SAMPLES, while every wavefront's bags fit
+// its lanes' bookkeeping and the LDS rows stay within kFusedLdsMax.
+constexpr int64_t kFusedLdsMax = 64 * 1024;
+int fused_samples(int num_slots, int64_t row_out_bytes) {
+  const int per_wave = (num_slots + kFusedWaves - 1) / kFusedWaves;
+  int spw = CTI_EBAG_FUSED_SAMPLES;
+  while (spw > 1 && (spw * per_wave > kFusedBagsPerWave || spw * row_out_bytes > kFusedLdsMax / 2)) spw /= 2;
+  return spw;
+}
+
+constexpr int64_t kFusedRowBytesMax = 64 * 1024;  // LDS copy of one output row
+constexpr int kFusedMaxSlots = 64;
+
+}  // namespace
+}  // namespace cti
+
+extern "C" int cti_ebag_fused_all_slots_layernorm(const void* values, int32_t index_type, const void* val_offsets,
+                                                  const void* row_offsets, int32_t offset_type, const void* weight,
+                                                  int32_t dtype, void* out, int64_t batch_size, int32_t num_slots,
+                                                  int32_t emb_dim, int64_t max_idx, int64_t nnz, int32_t pooling,
+                                                  const void* gamma, const void* beta, int32_t param_dtype, float eps,
+                                                  void* stream) {
+  clear_error();
+  if (index_type != CTI_EBAG_I64 && index_type != CTI_EBAG_I32)
+    return set_error(CTI_EBAG_EINVAL, "unknown index type code %d", index_type);
+  if (offset_type != CTI_EBAG_I64 && offset_type != CTI_EBAG_I32)
+    return set_error(CTI_EBAG_EINVAL, "unknown offset type code %d", offset_type);
+  if (!dtype_ok(dtype)) return set_error(CTI_EBAG_EINVAL, "unknown dtype code %d", dtype);
+  if (!dtype_ok(param_dtype)) return set_error(CTI_EBAG_EINVAL, "unknown parameter dtype code %d", param_dtype);
+  if (pooling != CTI_EBAG_SUM && pooling != CTI_EBAG_MEAN) return set_error(CTI_EBAG_EINVAL, "unknown pooling code %d", pooling);
+  if (batch_size < 0) return set_error(CTI_EBAG_EINVAL, "batch_size must be >= 0 (got %lld)", (long long)batch_size);
+  if (num_slots < 0) return set_error(CTI_EBAG_EINVAL, "num_slots must be >= 0 (got %d)", num_slots);
+  if (emb_dim < 1) return set_error(CTI_EBAG_EINVAL, "emb_dim must be >= 1 (got %d)", emb_dim);
+  if (max_idx < 0) return set_error(CTI_EBAG_EINVAL, "max_idx must be >= 0 (got %lld)", (long long)max_idx);
+  if (max_idx >= INT32_MAX) return set_error(CTI_EBAG_EUNSUPPORTED, "max_idx must be < 2^31 - 1 (got %lld)", (long long)max_idx);
+  if (nnz < 0) return set_error(CTI_EBAG_EINVAL, "nnz must be >= 0 (got %lld)", (long long)nnz);
+  if (!(eps >= 0.0f)) return set_error(CTI_EBAG_EINVAL, "eps must be >= 0");
+  if (batch_size == 0 || num_slots == 0) return CTI_EBAG_OK;
+  if (!val_offsets || !row_offsets || !weight || !out || !gamma || !beta || (nnz > 0 && !values))
+    return set_error(CTI_EBAG_EINVAL, "NULL device pointer among values/val_offsets/row_offsets/weight/out/gamma/beta");
+  // shapes the fused kernel covers; the caller runs pooling and LayerNorm separately otherwise
+  const int tb = dtype_bytes(dtype);
+  const int64_t row_bytes = static_cast<int64_t>(emb_dim) * tb;
+  if (dtype == CTI_EBAG_F16 || param_dtype == CTI_EBAG_F16)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "fused LayerNorm: fp16 tables or parameters");
+  if (num_slots > kFusedMaxSlots)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "fused LayerNorm: more than %d slots", kFusedMaxSlots);
+  if (row_bytes < 64 || row_bytes > 1024 || (row_bytes & (row_bytes - 1)) != 0)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "fused LayerNorm: table rows of %lld bytes (64..1024, a power of two)",
+                     (long long)row_bytes);
+  if (row_bytes * num_slots > kFusedRowBytesMax)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "fused LayerNorm: output rows over %lld bytes", (long long)kFusedRowBytesMax);
+  if (reinterpret_cast<uintptr_t>(weight) % 16 || reinterpret_cast<uintptr_t>(out) % 16 ||
+      reinterpret_cast<uintptr_t>(gamma) % 16 || reinterpret_cast<uintptr_t>(beta) % 16)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "fused LayerNorm: weight, out, gamma and beta must be 16-byte aligned");
+  const int lanes = static_cast<int>(row_bytes / 16);
+  PoolParams p;
+  memset(&p, 0, sizeof(p));
+  p.values = values;
+  p.idx32 = index_type == CTI_EBAG_I32;
+  p.offsets = row_offsets;
+  p.val_base = val_offsets;
+  p.off32 = offset_type == CTI_EBAG_I32;
+  p.offsets_stride = batch_size + 1;
+  p.nnz = nnz;
+  p.out = static_cast<char*>(out);
+  p.out_row_stride = static_cast<int64_t>(num_slots) * emb_dim;
+  p.batch = batch_size;
+  p.pooling = pooling;
+  p.num_fields = num_slots;
+  p.sub_threshold = CTI_EBAG_SUB_THRESHOLD;
+  p.block_threshold = kNoLimit;
+  p.split_threshold = kNoLimit;
+  const int64_t rows = max_idx + 1;
+  const int64_t span = (rows - 1) * row_bytes + row_bytes;
+  const bool fits = rows < (int64_t{1} << 32) / row_bytes;
+  for (int f = 0; f < num_slots; ++f) {
+    FieldDesc& d = p.f[f];
+    d.table = static_cast<const char*>(weight);
+    d.max_row = max_idx;
+    d.row_bytes = row_bytes;
+    d.dim = emb_dim;
+    d.out_col = f * emb_dim;
+    d.gidx = f;
+    d.span_bytes = fits ? static_cast<uint32_t>(span) : 0u;
+  }
+  p.buffer_ok = fits ? 1 : 0;
+  if (batch_size > INT32_MAX) return set_error(CTI_EBAG_EUNSUPPORTED, "batch_size must be < 2^31");
+  FusedNorm fn;
+  fn.gamma = gamma;
+  fn.beta = beta;
+  fn.eps = eps;
+  const size_t row_lds = static_cast<size_t>(row_bytes * num_slots);
+  const int spw = fused_samples(num_slots, row_bytes * num_slots);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (dtype == CTI_EBAG_F32)
+    e = param_dtype == CTI_EBAG_F32 ? launch_fused_lanes<float, float>(lanes, p, fn, spw, row_lds, st)
+                                    : launch_fused_lanes<float, bf16_t>(lanes, p, fn, spw, row_lds, st);
+  else
+    e = param_dtype == CTI_EBAG_F32 ? launch_fused_lanes<bf16_t, float>(lanes, p, fn, spw, row_lds, st)
+                                    : launch_fused_lanes<bf16_t, bf16_t>(lanes, p, fn, spw, row_lds, st);
+  if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "fused pooling + LayerNorm launch failed: %s", hipGetErrorString(e));
+  return CTI_EBAG_OK;
+}
 
 extern "C" int cti_ebag_fused_all_slots(const int64_t* values, const int64_t* val_offsets,
                                         const int64_t* row_offsets, const void* weight, int32_t dtype,

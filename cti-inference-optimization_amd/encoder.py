@@ -1,9 +1,10 @@
 """RepEncoder with the fused embedding step and the input LayerNorm on the HIP path.
 
 Mirrors the reference module online_best/infer.py:945-1100 (constructor signature, parameter
-names, forward(batch) contract): the 28 slots are pooled by ``fused_all_slots_embedding`` into
-``[B, slot_num*emb_dim]`` in the table's dtype, the rows are normalised by ``layer_norm`` with
-the ``input_norm`` parameters (the reference's Triton LayerNorm, online_best/infer.py:1061-1076),
+names, forward(batch) contract): the 28 slots are pooled into ``[B, slot_num*emb_dim]`` in the
+table's dtype and normalised with the ``input_norm`` parameters (the reference's Triton
+LayerNorm, online_best/infer.py:1061-1076) by one fused kernel
+(``fused_all_slots_embedding_layernorm``; ``pooled`` alone uses ``fused_all_slots_embedding``),
 and ``linear`` (torch's Linear, a plain library GEMM) maps them to d_model
 (online_best/infer.py:1084). Like the reference's Triton kernels, the pooling and the
 LayerNorm are forward-only (inference).
@@ -18,7 +19,8 @@ import torch
 from torch import nn
 
 from .layout import pack_slots
-from .ops import fused_all_slots_embedding, fused_all_slots_embedding_int8, layer_norm, quantize_embedding_int8
+from .ops import (fused_all_slots_embedding, fused_all_slots_embedding_int8, fused_all_slots_embedding_layernorm,
+                  layer_norm, quantize_embedding_int8)
 
 
 class RepEncoder(nn.Module):
@@ -75,11 +77,23 @@ class RepEncoder(nn.Module):
                                              batch_size, self.emb_dim, self.emb.num_embeddings - 1)
 
     def normalized(self, batch: dict) -> torch.Tensor:
-        """Pooled rows after the input LayerNorm: ``[B, slot_num*emb_dim]`` in the table dtype."""
-        fused_embs = self.pooled(batch)
+        """Pooled rows after the input LayerNorm: ``[B, slot_num*emb_dim]`` in the table dtype.
+
+        With the float table, pooling and LayerNorm run as one kernel (the pooled row stays on
+        chip); with the int8 table, the int8 pooling is followed by the LayerNorm kernel.
+        """
         norm = self.input_norm
+        if self._int8_weight is not None:
+            fused_embs = self.pooled(batch)
+            with torch.no_grad():
+                return layer_norm(fused_embs, norm.weight.detach(), norm.bias.detach(), norm.eps, out=fused_embs)
+        flat_values, val_offsets, flat_row_offsets, batch_size = self.flat_inputs(batch)
+        weight = self.emb.weight
+        out = torch.empty((batch_size, self.slot_num * self.emb_dim), device=weight.device, dtype=weight.dtype)
         with torch.no_grad():
-            return layer_norm(fused_embs, norm.weight.detach(), norm.bias.detach(), norm.eps, out=fused_embs)
+            return fused_all_slots_embedding_layernorm(flat_values, val_offsets, flat_row_offsets, weight.detach(), out,
+                                                       batch_size, self.emb_dim, self.emb.num_embeddings - 1,
+                                                       norm.weight.detach(), norm.bias.detach(), norm.eps)
 
     def forward(self, batch: dict) -> torch.Tensor:
         return self.linear(self.normalized(batch))

@@ -263,6 +263,75 @@ def fused_all_slots_embedding(
     return out
 
 
+def fused_all_slots_embedding_layernorm(
+    flat_values: torch.Tensor,
+    val_offsets: torch.Tensor,
+    flat_row_offsets: torch.Tensor,
+    weight: torch.Tensor,
+    out: torch.Tensor,
+    batch_size: int,
+    emb_dim: int,
+    max_idx: int,
+    ln_weight: torch.Tensor,
+    ln_bias: torch.Tensor,
+    eps: float = 1e-5,
+    pooling: str = "sum",
+) -> torch.Tensor:
+    """The fused embedding step followed by the input LayerNorm (online_best/infer.py:1050-1076):
+    ``out[B, S*emb_dim] = LayerNorm(pool)``, pool as ``fused_all_slots_embedding`` writes it
+    (``pooling='sum'`` as the reference; 'mean' also accepted), the LayerNorm with fp32 statistics
+    over each row and ``ln_weight`` / ``ln_bias`` of ``S*emb_dim`` elements.
+
+    One kernel keeps each pooled row on chip and writes only the normalised row. Shapes the fused
+    kernel does not cover (see ``cti_ebag_fused_all_slots_layernorm``) run the pooling kernel and
+    the LayerNorm kernel one after the other (same result within the LayerNorm's fp32 rounding).
+    Returns ``out``.
+    """
+    dev = weight.device
+    _require_device_tensor("weight", weight)
+    icode, ocode = _check_flat_layout(flat_values, val_offsets, flat_row_offsets, out, dev)
+    val_offsets = _same_offset_type(val_offsets, flat_row_offsets, flat_values.numel())
+    if weight.dim() != 2 or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous 2-D tensor")
+    batch_size, emb_dim, max_idx = int(batch_size), int(emb_dim), int(max_idx)
+    num_slots = val_offsets.numel()
+    if weight.shape[1] != emb_dim:
+        raise ValueError(f"weight has {weight.shape[1]} columns, emb_dim is {emb_dim}")
+    if not 0 <= max_idx < weight.shape[0]:
+        raise ValueError(f"max_idx {max_idx} outside [0, {weight.shape[0] - 1}]")
+    if flat_row_offsets.numel() != num_slots * (batch_size + 1):
+        raise ValueError(f"flat_row_offsets has {flat_row_offsets.numel()} entries, expected "
+                         f"{num_slots} * ({batch_size} + 1)")
+    if out.dtype != weight.dtype or tuple(out.shape) != (batch_size, num_slots * emb_dim):
+        raise ValueError(f"out must be ({batch_size}, {num_slots * emb_dim}) {weight.dtype}")
+    width = num_slots * emb_dim
+    for name, t in (("ln_weight", ln_weight), ("ln_bias", ln_bias)):
+        _require_device_tensor(name, t, dev)
+        _require_contiguous(name, t)
+        if t.numel() != width:
+            raise ValueError(f"{name} has {t.numel()} elements, expected {width}")
+    if ln_weight.dtype != ln_bias.dtype:
+        raise TypeError("ln_weight and ln_bias dtypes differ")
+    lib = _capi.lib()
+    with torch.cuda.device(dev):
+        rc = lib.cti_ebag_fused_all_slots_layernorm(
+            flat_values.data_ptr(), icode, val_offsets.data_ptr(), flat_row_offsets.data_ptr(), ocode,
+            weight.data_ptr(), _capi.dtype_code(weight.dtype), out.data_ptr(), batch_size, num_slots, emb_dim,
+            max_idx, flat_values.numel(), _capi.pooling_code(pooling), ln_weight.data_ptr(), ln_bias.data_ptr(),
+            _capi.dtype_code(ln_weight.dtype), float(eps), _capi.current_stream_handle(dev))
+        if rc == _capi.EUNSUPPORTED:
+            if pooling != "sum":
+                raise _capi.EbagError(rc, _capi.last_error() + " (the unfused fallback pools by sum only)")
+            code = _capi.dtype_code(weight.dtype)
+            _capi.check(lib.cti_ebag_fused_all_slots_typed(
+                flat_values.data_ptr(), icode, val_offsets.data_ptr(), flat_row_offsets.data_ptr(), ocode,
+                weight.data_ptr(), code, None, out.data_ptr(), code, batch_size, num_slots, emb_dim, max_idx,
+                flat_values.numel(), _capi.current_stream_handle(dev)))
+            return layer_norm(out, ln_weight, ln_bias, eps, out=out)
+        _capi.check(rc)
+    return out
+
+
 def fused_embedding(batch: dict, weight: torch.Tensor, slot_num: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The fused embedding step of RepEncoder.forward (online_best/infer.py:1029-1059) on a
     batch dict holding ``_flat_values``, ``_flat_row_offsets`` and ``_val_offsets``.

@@ -222,6 +222,26 @@ int cti_ebag_fused_all_slots_typed(const void* values, int32_t index_type, const
                                    int64_t nnz, void* stream);
 
 /*
+ * The reference-layout pooling with the encoder's input LayerNorm fused into the writer
+ * (online_best/infer.py:1050-1076: the pooled block `fused_embs` [B, S*D] and
+ * layernorm_forward_kernel over its rows, :829-858): out[b] = LayerNorm(pool(b)), where pool(b)
+ * is the row cti_ebag_fused_all_slots_typed would write (`pooling` CTI_EBAG_SUM as in the
+ * reference, or CTI_EBAG_MEAN), rounded to `dtype`, and the LayerNorm takes fp32 mean and variance
+ * over the row's S*D values, y = (x - mean) * rstd * gamma + beta, rounded once to `dtype`.
+ * gamma, beta: [S*D] of `param_dtype`. The pooled row is kept on chip; only the normalised row is
+ * written. Covered shapes: F32 / BF16 tables and parameters, table rows of 64..1024 bytes (a
+ * power of two), S <= 64, S*D*sizeof(dtype) <= 64 KiB, 16-byte aligned weight / out / gamma /
+ * beta; otherwise CTI_EBAG_EUNSUPPORTED (run cti_ebag_fused_all_slots_typed and
+ * cti_ebag_layernorm instead).
+ */
+int cti_ebag_fused_all_slots_layernorm(const void* values, int32_t index_type, const void* val_offsets,
+                                       const void* row_offsets, int32_t offset_type, const void* weight,
+                                       int32_t dtype, void* out, int64_t batch_size, int32_t num_slots,
+                                       int32_t emb_dim, int64_t max_idx, int64_t nnz, int32_t pooling,
+                                       const void* gamma, const void* beta, int32_t param_dtype, float eps,
+                                       void* stream);
+
+/*
  * Host-side compaction of sign ids for the transfer to the device (replaces the int64
  * `.to(device, non_blocking=True)` of `_flat_values` at online_best/infer.py:745-746; the comment
  * at :744 names the int32 form). `src` and `dst` are HOST pointers (dst typically pinned):

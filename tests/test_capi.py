@@ -22,7 +22,8 @@ def test_header_declares_the_entry_points():
     for n in ("cti_ebag_fused_all_slots", "cti_ebag_forward", "cti_ebag_pack_slots", "cti_ebag_merge_batches",
               "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version", "cti_ebag_layernorm",
               "cti_ebag_fused_all_slots_int8", "cti_ebag_quantize_int8", "cti_ebag_fused_all_slots_typed",
-              "cti_ebag_narrow_ids", "cti_ebag_stage_copy", "cti_ebag_stage_offset"):
+              "cti_ebag_narrow_ids", "cti_ebag_stage_copy", "cti_ebag_stage_offset",
+              "cti_ebag_fused_all_slots_layernorm"):
         assert n in names
 
 
