@@ -22,6 +22,12 @@ shared table as in the reference, sum pooling): the pooling kernel followed by t
 kernel, against the fused kernel that normalises each pooled row on chip
 (online_best/infer.py:1050-1076).
 
+`--stage layout` times the device layout kernels against the reference's way of doing the same
+work: merging the 8 sub-batches of lazy-32k into one flat layout (online_best/infer.py:581-631,
+torch ops on host tensors there; one kernel over device tensors here) and packing 28 per-slot
+(values, offsets) pairs of a bf16-2m batch into the flat layout (online_best/infer.py:960-974,
+two torch.cat and a host list copied to the device there; one kernel here).
+
 `--stage layernorm` times the encoder's input LayerNorm instead (online_best/infer.py:1061-1076):
 the workload's batches are pooled once, and each step normalises one pooled block
 [B, sum(D)] (rows/s; roofline bytes = the block read and written plus gamma and beta).
@@ -308,6 +314,153 @@ def bench_encoder(args, pkg, wls, dev):
     print(json.dumps(rec), flush=True)
 
 
+def reference_merge_cpu(batches, slot_num=28):
+    """The flat-layout part of _timed_lazy_merge_group_cpu (online_best/infer.py:592-620) on host
+    tensors: per slot, slice each sub-batch, rebase its local offsets, concatenate."""
+    import torch
+
+    parts_v, parts_o, vo = [], [], [0]
+    for slot in range(slot_num):
+        sv, so = [], []
+        base = 0
+        for b in batches:
+            vals, ro, vos = b["_flat_values"], b["_flat_row_offsets"], b["_val_offsets"]
+            seq_len = ro.numel() // slot_num - 1
+            start = int(vos[slot])
+            end = int(vos[slot + 1]) if slot + 1 < slot_num else int(vals.numel())
+            sv.append(vals[start:end])
+            so.append(ro[slot * (seq_len + 1):(slot + 1) * (seq_len + 1)][:-1] + base)
+            base += end - start
+        parts_v.append(torch.cat(sv).long())
+        parts_o.append(torch.cat(so + [torch.tensor([base], dtype=torch.long)]).long())
+        vo.append(vo[-1] + base)
+    return {"_flat_values": torch.cat(parts_v).long(), "_flat_row_offsets": torch.cat(parts_o).long(),
+            "_val_offsets": torch.tensor(vo[:-1], dtype=torch.long)}
+
+
+def reference_pack(slots, dev):
+    """online_best/infer.py:960-974 on device slot tensors: two torch.cat and val_offsets built
+    from the slot sizes on the host, then copied to the device."""
+    import torch
+
+    val_lens = [0]
+    for v, _ in slots:
+        val_lens.append(val_lens[-1] + v.shape[0])
+    return {"_flat_values": torch.cat([v for v, _ in slots]), "_flat_row_offsets": torch.cat([o for _, o in slots]),
+            "_val_offsets": torch.tensor(val_lens[:-1], device=dev, dtype=torch.long)}
+
+
+def bench_layout(args, pkg, dev):
+    """Device merge and pack kernels against the reference's merge (host) and pack (torch.cat)."""
+    import numpy as np
+    import torch
+
+    W = pkg.workloads
+
+    def flat(wl, device):
+        F, B = wl.num_fields, wl.batch
+        off = wl.offsets
+        ro = np.stack([off[f * B:(f + 1) * B + 1] - off[f * B] for f in range(F)]).reshape(-1)
+        return {"_flat_values": torch.from_numpy(wl.values).to(device),
+                "_flat_row_offsets": torch.from_numpy(ro).to(device),
+                "_val_offsets": torch.from_numpy(off[0:F * B:B].copy()).to(device)}
+
+    def same(a, b):
+        return all(torch.equal(a[k].cpu(), b[k].cpu()) for k in ("_flat_values", "_flat_row_offsets", "_val_offsets"))
+
+    def gpu_timed(fn, K):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(K):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / K, e0.elapsed_time(e1) / 1e3 / K
+
+    def host_timed(fn, seconds):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            if time.perf_counter() - t0 > seconds:
+                return (time.perf_counter() - t0) / n
+
+    log("lazy-32k: generating the 8 sub-batches")
+    lazy = W.make("lazy-32k", seed=1)
+    host_subs = [flat(s, "cpu") for s in lazy.sub_batches]
+    dev_subs = [flat(s, dev) for s in lazy.sub_batches]
+    F = lazy.num_fields
+    merged_ref = reference_merge_cpu(host_subs, F)
+    if not same(merged_ref, pkg.merge_batches(dev_subs, F)):
+        raise RuntimeError("device merge differs from the reference merge")
+    log("timing the reference merge on the host")
+    t_ref_merge = host_timed(lambda: reference_merge_cpu(host_subs, F), 3.0)
+    log("timing the device merge")
+    wall_merge, k_merge_py = gpu_timed(lambda: pkg.merge_batches(dev_subs, F), args.steps)
+    # the raw C call with its argument arrays built once (what a serving loop would do)
+    lay, lib, C = pkg.layout, pkg._capi.lib(), pkg._capi
+    merged = pkg.merge_batches(dev_subs, F)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    margs = (lay._ptr_array([d["_flat_values"] for d in dev_subs]), lay._ptr_array([d["_val_offsets"] for d in dev_subs]),
+             lay._ptr_array([d["_flat_row_offsets"] for d in dev_subs]),
+             lay._i64_array([d["_flat_row_offsets"].numel() // F - 1 for d in dev_subs]),
+             lay._i64_array([d["_flat_values"].numel() for d in dev_subs]), len(dev_subs), F,
+             merged["_flat_values"].data_ptr(), merged["_flat_row_offsets"].data_ptr(),
+             merged["_val_offsets"].data_ptr(), None, stream)
+    wall_merge_raw, k_merge = gpu_timed(lambda: C.check(lib.cti_ebag_merge_batches(*margs)), args.steps)
+    n_vals, n_offs = lazy.nnz, F * (lazy.batch + 1)
+    merge_bytes = 16 * n_vals + 8 * sum(s["_flat_row_offsets"].numel() for s in host_subs) + 8 * n_offs + 16 * F
+
+    log("bf16-2m: per-slot pairs on the device")
+    wl = W.make("bf16-2m", seed=1)
+    B = wl.batch
+    slots = []
+    for f in range(F):
+        o = wl.offsets[f * B:(f + 1) * B + 1]
+        slots.append((torch.from_numpy(wl.values[o[0]:o[-1]].copy()).to(dev), torch.from_numpy(o - o[0]).to(dev)))
+    if not same(reference_pack(slots, dev), pkg.pack_slots(slots)):
+        raise RuntimeError("device pack differs from the reference pack")
+    log("timing the reference pack and the device pack")
+    wall_ref_pack, k_ref_pack = gpu_timed(lambda: reference_pack(slots, dev), args.steps)
+    wall_pack, k_pack_py = gpu_timed(lambda: pkg.pack_slots(slots), args.steps)
+    packed = pkg.pack_slots(slots)
+    pargs = (lay._ptr_array([v for v, _ in slots]), lay._ptr_array([o for _, o in slots]),
+             lay._i64_array([v.numel() for v, _ in slots]), F, B, packed["_flat_values"].data_ptr(),
+             packed["_flat_row_offsets"].data_ptr(), packed["_val_offsets"].data_ptr(), None, stream)
+    wall_pack_raw, k_pack = gpu_timed(lambda: C.check(lib.cti_ebag_pack_slots(*pargs)), args.steps)
+    pack_bytes = 16 * wl.nnz + 16 * F * (B + 1) + 8 * F
+
+    achieved = merge_bytes / k_merge / 1e9
+    rec = {
+        "metric": "flat-layout merge of 8 sub-batches (lazy-32k, 28 fields, B=8x4096) and per-slot pack "
+                  "(bf16-2m batch): bags/s",
+        "value": lazy.batch * F / wall_merge_raw,
+        "unit": "bags/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall_merge_raw * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+        "data": "synthetic: lazy-32k sub-batches and one bf16-2m batch (seed 1)",
+        "config": {"workload": "lazy-32k merge (8 x 4096 samples, 28 fields, nnz "
+                               f"{n_vals}) and bf16-2m per-slot pack (4096 samples, nnz {wl.nnz})"},
+        "us_per_call": {"reference_merge_host": t_ref_merge * 1e6, "device_merge_python": wall_merge * 1e6,
+                        "device_merge_raw": wall_merge_raw * 1e6, "device_merge_gpu": k_merge * 1e6,
+                        "reference_pack": wall_ref_pack * 1e6, "reference_pack_gpu": k_ref_pack * 1e6,
+                        "device_pack_python": wall_pack * 1e6, "device_pack_raw": wall_pack_raw * 1e6,
+                        "device_pack_gpu": k_pack * 1e6},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "merge_kernel",
+                     "bytes_per_launch": merge_bytes, "launch_us_mean": k_merge * 1e6,
+                     "pack_bytes_per_launch": pack_bytes, "pack_achieved": pack_bytes / k_pack / 1e9},
+        "cpu_baseline": {"value": lazy.batch * F / t_ref_merge, "unit": "bags/s", "cores": torch.get_num_threads(),
+                         "kind": "port", "sample": "the reference merge (torch ops on host tensors) of the same "
+                                                   "8 sub-batches, repeated for 3 s"},
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def bench_layernorm(args, pkg, plan, inputs, wl0, dev):
     """Time the input LayerNorm over pooled blocks of the workload (one block per step, rotated)."""
     import torch
@@ -365,7 +518,7 @@ def main():
     ap.add_argument("--bins", action="store_true", help="run the device length-binning pass")
     ap.add_argument("--block-threshold", type=int, default=0)
     ap.add_argument("--split-threshold", type=int, default=0)
-    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d", "encoder"],
+    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d", "encoder", "layout"],
                     help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
                          "step end to end from host batches")
     ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
@@ -400,6 +553,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.stage == "layout":
+        return bench_layout(args, pkg, dev)
     log(f"workload {args.workload}: generating {args.sets} index sets")
     wls = [W.make(args.workload, seed=s) for s in range(1, args.sets + 1)]
     wl0 = wls[0]

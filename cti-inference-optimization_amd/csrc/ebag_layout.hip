@@ -19,6 +19,29 @@ constexpr int kThreads = 256;
 constexpr int kMaxSlots = 64;
 constexpr int kMaxSub = 32;
 
+// Two int64 moved as one 16-byte access (the arrays are 8-byte aligned; the hardware takes
+// multi-dword accesses at dword alignment).
+struct __attribute__((aligned(8))) I64Pair {
+  int64_t a, b;
+};
+
+// dst[i] = src[i] + add for i < n; grid-stride item j covers elements 2j and 2j+1.
+__device__ __forceinline__ void copy_add_i64(const int64_t* __restrict__ src, int64_t* __restrict__ dst, int64_t n,
+                                             int64_t add, int64_t j0, int64_t stride) {
+  for (int64_t j = j0; 2 * j < n; j += stride) {
+    const int64_t e = 2 * j;
+    if (e + 1 < n) {
+      I64Pair v;
+      __builtin_memcpy(&v, src + e, sizeof(v));
+      v.a += add;
+      v.b += add;
+      __builtin_memcpy(dst + e, &v, sizeof(v));
+    } else {
+      dst[e] = src[e] + add;
+    }
+  }
+}
+
 struct PackParams {
   const int64_t* vals[kMaxSlots];
   const int64_t* offs[kMaxSlots];
@@ -45,13 +68,10 @@ __global__ void __launch_bounds__(kThreads) pack_kernel(const PackParams p) {
   const int64_t* __restrict__ src_o = p.offs[si];
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  for (int64_t i = i0; i < n; i += stride) p.flat_values[vb + i] = src_v[i];
+  copy_add_i64(src_v, p.flat_values + vb, n, 0, i0, stride);
   const int64_t B = p.batch;
-  for (int64_t i = i0; i <= B; i += stride) {
-    const int64_t o = src_o[i];
-    p.flat_row_offsets[static_cast<int64_t>(s) * (B + 1) + i] = o;
-    if (p.global_offsets && i < B) p.global_offsets[static_cast<int64_t>(s) * B + i] = vb + o;
-  }
+  copy_add_i64(src_o, p.flat_row_offsets + static_cast<int64_t>(s) * (B + 1), B + 1, 0, i0, stride);
+  if (p.global_offsets) copy_add_i64(src_o, p.global_offsets + static_cast<int64_t>(s) * B, B, vb, i0, stride);
   if (i0 == 0) {
     p.val_offsets[s] = vb;
     if (p.global_offsets && s == p.all_slots - 1) p.global_offsets[static_cast<int64_t>(p.all_slots) * B] = p.total;
@@ -74,19 +94,31 @@ struct MergeParams {
   int32_t num_slots;
 };
 
+// Slot s of sub-batch k: values [slot_start, slot_start + slot_nnz), its val_offsets entries
+// clamped to [0, nnz] (a malformed entry yields an empty or shortened slot, never a read outside
+// the sub-batch's values).
+__device__ __forceinline__ int64_t slot_start(const MergeParams& p, int s, int k) {
+  return clamp_i64(p.vo[k][s], 0, p.nnz[k]);
+}
 __device__ __forceinline__ int64_t slot_nnz(const MergeParams& p, int s, int k) {
-  const int64_t a = p.vo[k][s];
-  const int64_t e = s + 1 < p.num_slots ? p.vo[k][s + 1] : p.nnz[k];
+  const int64_t a = slot_start(p, s, k);
+  const int64_t e = s + 1 < p.num_slots ? clamp_i64(p.vo[k][s + 1], a, p.nnz[k]) : p.nnz[k];
   return e - a;
 }
 
 // grid: (chunks, num_slots * num_sub); block (x, s*K + k) copies slot s of sub-batch k.
 __global__ void __launch_bounds__(kThreads) merge_kernel(const MergeParams p) {
-  __shared__ int64_t s_red[3][kThreads];
+  __shared__ int64_t s_red[3][kThreads / kWave];
   const int K = p.num_sub;
   const int s = static_cast<int>(blockIdx.y) / K;
   const int k = static_cast<int>(blockIdx.y) % K;
   const int t = static_cast<int>(threadIdx.x);
+  // The grid is sized for the largest slot; a workgroup past this slot's values and offsets
+  // (two per thread per grid-stride item) has nothing to copy. Workgroup 0 always stays: it
+  // writes the slot's closing entries.
+  const int64_t n_here = slot_nnz(p, s, k);
+  const int64_t work = n_here > p.bsub[k] ? n_here : p.bsub[k];
+  if (blockIdx.x > 0 && static_cast<int64_t>(blockIdx.x) * kThreads * 2 >= work) return;
 
   // before: values of slots < s (all sub-batches); vb: slot s of sub-batches < k; tot: slot s.
   int64_t before = 0, vb = 0, tot = 0;
@@ -100,43 +132,45 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const MergeParams p) {
       if (kk < k) vb += c;
     }
   }
-  s_red[0][t] = before;
-  s_red[1][t] = vb;
-  s_red[2][t] = tot;
-  __syncthreads();
-  for (int w = kThreads / 2; w > 0; w >>= 1) {
-    if (t < w) {
-      s_red[0][t] += s_red[0][t + w];
-      s_red[1][t] += s_red[1][t + w];
-      s_red[2][t] += s_red[2][t + w];
-    }
-    __syncthreads();
+  // wavefront sums (xor butterfly), then the wavefronts' sums through LDS (one barrier)
+  const int lane = lane_id();
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) {
+    before += shfl_i64(before, lane ^ m);
+    vb += shfl_i64(vb, lane ^ m);
+    tot += shfl_i64(tot, lane ^ m);
   }
-  before = s_red[0][0];
-  vb = s_red[1][0];
-  tot = s_red[2][0];
+  constexpr int kWaves = kThreads / kWave;
+  if (lane == 0) {
+    s_red[0][t / kWave] = before;
+    s_red[1][t / kWave] = vb;
+    s_red[2][t / kWave] = tot;
+  }
+  __syncthreads();
+  before = vb = tot = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    before += s_red[0][w];
+    vb += s_red[1][w];
+    tot += s_red[2][w];
+  }
 
   const int64_t B = p.batch;
   const int64_t Bk = p.bsub[k];
-  const int64_t n = slot_nnz(p, s, k);
-  const int64_t src0 = p.vo[k][s];
+  const int64_t n = n_here;
+  const int64_t src0 = slot_start(p, s, k);
   const int64_t dst0 = before + vb;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kThreads + t;
-  const int64_t* __restrict__ sv = p.vals[k];
   const int64_t* __restrict__ so = p.ro[k] + static_cast<int64_t>(s) * (Bk + 1);
-  for (int64_t i = i0; i < n; i += stride) p.flat_values[dst0 + i] = sv[src0 + i];
-  int64_t* ro_out = p.flat_row_offsets + static_cast<int64_t>(s) * (B + 1) + p.bbase[k];
-  int64_t* g_out = p.global_offsets ? p.global_offsets + static_cast<int64_t>(s) * B + p.bbase[k] : nullptr;
-  for (int64_t i = i0; i < Bk; i += stride) {
-    const int64_t o = so[i] + vb;
-    ro_out[i] = o;
-    if (g_out) g_out[i] = before + o;
-  }
+  copy_add_i64(p.vals[k] + src0, p.flat_values + dst0, n, 0, i0, stride);
+  copy_add_i64(so, p.flat_row_offsets + static_cast<int64_t>(s) * (B + 1) + p.bbase[k], Bk, vb, i0, stride);
+  if (p.global_offsets)
+    copy_add_i64(so, p.global_offsets + static_cast<int64_t>(s) * B + p.bbase[k], Bk, before + vb, i0, stride);
   if (i0 == 0) {
     if (k == K - 1) p.flat_row_offsets[static_cast<int64_t>(s) * (B + 1) + B] = tot;
     if (k == 0) p.val_offsets[s] = before;
-    if (g_out && k == 0 && s == p.num_slots - 1)
+    if (p.global_offsets && k == 0 && s == p.num_slots - 1)
       p.global_offsets[static_cast<int64_t>(p.num_slots) * B] = before + tot;
   }
 }

@@ -179,7 +179,10 @@ int cti_ebag_pack_slots(const int64_t* const* slot_values, const int64_t* const*
  *   flat_values int64 [sum sub_nnz], flat_row_offsets int64 [num_slots*(B+1)],
  *   val_offsets int64 [num_slots]; optional global_offsets int64 [num_slots*B+1].
  * Slot s of sub-batch k spans sub_values[k][val_offsets_k[s] : val_offsets_k[s+1]]
- * (the last slot ends at sub_nnz[k]), as at online_best/infer.py:604-606.
+ * (the last slot ends at sub_nnz[k]), as at online_best/infer.py:604-606. val_offsets_k must be
+ * non-decreasing within [0, sub_nnz[k]]; an entry outside that range is clamped into it (the
+ * slot shrinks, nothing outside the sub-batch is read), where the reference's Python slicing
+ * would wrap a negative entry.
  */
 int cti_ebag_merge_batches(const int64_t* const* sub_values,
                            const int64_t* const* sub_val_offsets,
