@@ -207,6 +207,47 @@ def test_fused_all_slots_int8_rejects_bad_arguments(pkg):
     assert c.lib().cti_ebag_fused_all_slots(256, 256, 256, 256, c.I8, 256, 4, 28, 128, 10, 5, None) == c.EINVAL
 
 
+def test_fused_layernorm_rejects_bad_arguments(pkg):
+    """Every case fails a host-side check, so nothing is launched (the pointers are not real)."""
+    c = pkg._capi
+    f = c.lib().cti_ebag_fused_all_slots_layernorm
+
+    def call(**kw):
+        a = dict(values=256, it=c.I64, vo=256, ro=256, ot=c.I64, weight=256, dt=c.BF16, out=256, B=4, S=28, D=128,
+                 max_idx=10, nnz=5, pooling=c.SUM, gamma=256, beta=256, pdt=c.F32, eps=1e-5)
+        a.update(kw)
+        return f(a["values"], a["it"], a["vo"], a["ro"], a["ot"], a["weight"], a["dt"], a["out"], a["B"], a["S"],
+                 a["D"], a["max_idx"], a["nnz"], a["pooling"], a["gamma"], a["beta"], a["pdt"], a["eps"], None)
+
+    assert call(it=7) == c.EINVAL and "index type" in c.last_error()
+    assert call(ot=7) == c.EINVAL and "offset type" in c.last_error()
+    assert call(dt=9) == c.EINVAL
+    assert call(pdt=9) == c.EINVAL and "parameter dtype" in c.last_error()
+    assert call(pooling=5) == c.EINVAL
+    assert call(B=-1) == c.EINVAL
+    assert call(D=0) == c.EINVAL
+    assert call(eps=-1.0) == c.EINVAL and call(eps=float("nan")) == c.EINVAL
+    assert call(max_idx=2 ** 31) == c.EUNSUPPORTED
+    assert call(gamma=None) == c.EINVAL and "NULL" in c.last_error()
+    assert call(dt=c.F16) == c.EUNSUPPORTED and "fp16" in c.last_error()
+    assert call(pdt=c.F16) == c.EUNSUPPORTED
+    assert call(S=65) == c.EUNSUPPORTED and "slots" in c.last_error()
+    assert call(D=8) == c.EUNSUPPORTED and "bytes" in c.last_error()  # 16-byte bf16 rows
+    assert call(D=48) == c.EUNSUPPORTED  # 96-byte rows: not a power of two
+    assert call(dt=c.F32, D=512) == c.EUNSUPPORTED and "2048 bytes" in c.last_error()
+    assert call(weight=264) == c.EUNSUPPORTED and "aligned" in c.last_error()
+    assert call(gamma=264) == c.EUNSUPPORTED
+    assert call(values=None, vo=None, ro=None, weight=None, out=None, gamma=None, beta=None, B=0, nnz=0) == c.OK
+
+
+def test_fused_layernorm_python_wrapper_validates_before_any_launch(pkg):
+    z = torch.zeros(5, dtype=torch.int64)
+    w = torch.zeros(10, 32)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        pkg.fused_all_slots_embedding_layernorm(z, torch.zeros(2, dtype=torch.int64), torch.zeros(8, dtype=torch.int64),
+                                                w, torch.zeros(3, 64), 3, 32, 9, torch.ones(64), torch.zeros(64))
+
+
 def test_quantize_int8_rejects_bad_arguments(pkg):
     c = pkg._capi
     f = c.lib().cti_ebag_quantize_int8
