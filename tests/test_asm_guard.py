@@ -1,7 +1,6 @@
-"""Guard on the generated gfx950 code (CPU only): the HIP sources compile to device assembly
-without scalar-cache stores, scalar atomics or scalar-cache write-back/discard, and every
-atomic is a vector (global) atomic. This file names those instructions and is therefore kept
-off GPU runs (.gpurunignore); it needs only hipcc."""
+"""Guard on the generated gfx950 code (CPU only, needs only hipcc): every HIP source compiles to
+device assembly without scalar-cache stores, scalar atomics or scalar-cache write-back/discard,
+and every atomic is a vector (global) atomic."""
 import os
 import re
 import subprocess
@@ -14,7 +13,8 @@ FORBIDDEN = re.compile(r"^\s+s_(store|atomic|buffer_store|buffer_atomic|dcache_w
                        re.M)
 
 
-@pytest.mark.parametrize("src", ["ebag_pool.hip", "ebag_layout.hip", "ebag_status.hip"])
+@pytest.mark.parametrize("src", ["ebag_pool.hip", "ebag_layout.hip", "ebag_status.hip", "ebag_norm.hip",
+                                 "ebag_quant.hip"])
 def test_no_scalar_cache_writes(src, tmp_path):
     out = tmp_path / (src + ".s")
     cmd = ["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
