@@ -24,7 +24,8 @@
 //     own bags are done (measured: multi-wavefront workgroups are slower, also when they share a
 //     length ranking). Row ids are clamped, narrowed to 32 bits (tables have < 2^31 rows) and
 //     broadcast through LDS; a step reads ROWS_IN_FLIGHT ids, then issues that many row loads
-//     before consuming any. Tables under 4 GiB with power-of-two row sizes are read with buffer
+//     before consuming any. A bag's ids are loaded one chunk ahead, so the next chunk's id load
+//     completes under the current chunk's row loads. Tables under 4 GiB with power-of-two row sizes are read with buffer
 //     loads: a row's offset is one shift-add, and rows past a bag's end use an out-of-range offset
 //     that returns zeros without a memory request (no per-row branch).
 //   * Mean: one fp64 reciprocal per bag, RN32(RN64(sum * 1/L)) per element, which equals the IEEE
@@ -68,6 +69,9 @@ namespace {
 #ifndef CTI_EBAG_ROUNDS
 #define CTI_EBAG_ROUNDS 2  // rounds of R length-ranked bags per tile of the main kernel
 #endif
+#ifndef CTI_EBAG_ID_PREFETCH
+#define CTI_EBAG_ID_PREFETCH 1  // load a bag's next chunk of row ids while the current chunk's rows load
+#endif
 
 constexpr int kMainThreads = kWave;  // main kernel: one wavefront per workgroup
 constexpr int kBinThreads = 256;
@@ -102,7 +106,12 @@ enum Variant : int {
   kVarL64V4 = 8,
   kVarGeneric = 9,
   kNumVariants = 10,
+  kVarMixed = 10,  // fields of several of the shapes kMixedLo..kMixedHi in one launch sequence
 };
+// Shapes a mixed-width launch covers: 4 to 64 lanes of one vector per row, i.e. rows of 64 B to
+// 1 KB (bf16 D = 32..512, fp32 D = 16..256, int8 D = 32..512). Each shape the kernels switch
+// over adds registers; rows of 16 or 32 B keep launches of their own.
+constexpr int kMixedLo = 2, kMixedHi = 6;
 
 struct FieldDesc {
   const char* table;   // row 0 of the field's table
@@ -113,6 +122,8 @@ struct FieldDesc {
   int32_t out_col;     // first output column
   int32_t gidx;        // field index used for offsets / val_base
   uint32_t span_bytes; // bytes from row 0 to the end of the last row, when below 4 GiB (else 0)
+  int32_t lanes_log2;  // mixed-width launches: the field's rows are 1 << lanes_log2 lanes x one vector
+  int32_t tile_begin;  // mixed-width launches: the field's first tile (fields in tile order)
 };
 
 struct PoolParams {
@@ -143,15 +154,19 @@ struct PoolParams {
 // Two lists share the workspace's entry array: bags pooled by one wavefront each grow from the
 // front, bags split over a workgroup's wavefronts grow from the back (together they never exceed
 // the number of bags of a launch, which the array holds).
+// Each entry also carries the bag's value range, so the list kernel needs no offset lookup.
 struct LongList {
   unsigned int* count;   // one-wavefront list length, incremented by the binning pass
   unsigned int* total;   // its snapshot read by the list kernel
   unsigned int* count2;  // split list length
   unsigned int* total2;
   int64_t* bags;         // entries: (local field index << 40) | sample index
-  int64_t capacity;      // entries in `bags`; split entry j is bags[capacity - 1 - j]
+  int64_t* starts;       // entry i's bag is values[starts[i], ends[i])
+  int64_t* ends;
+  int64_t capacity;      // entries in each array; split entry j is at index capacity - 1 - j
 };
 constexpr int64_t kWorkspaceHeader = 256;
+static_assert(sizeof(PoolParams) + sizeof(LongList) <= 4096, "kernel arguments must fit in 4 KB");
 
 __device__ __forceinline__ int xcd_contiguous(int bid, int n) {
   // Hardware deals workgroups to the 8 XCDs round-robin; map XCD x to one contiguous range.
@@ -233,8 +248,18 @@ __device__ __forceinline__ void wave_slice_partial(const PoolParams& p, const ch
   using S = Shape<TT, LANES, VPL>;
   const int lane = lane_id();
   const int g = lane / LANES, sl = lane % LANES;
+#if CTI_EBAG_ID_PREFETCH
+  int64_t next_id = s0 + lane < s1 ? load_index(p, s0 + lane) : 0;
+#endif
   for (int64_t c = s0; c < s1; c += kWave) {
-    ids[lane] = c + lane < s1 ? static_cast<unsigned int>(clamp_i64(load_index(p, c + lane), 0, max_row)) : 0u;
+#if CTI_EBAG_ID_PREFETCH
+    // ids one chunk ahead: the next chunk's id load overlaps this chunk's row loads
+    const int64_t id = next_id;
+    if (c + kWave + lane < s1) next_id = load_index(p, c + kWave + lane);
+#else
+    const int64_t id = c + lane < s1 ? load_index(p, c + lane) : 0;
+#endif
+    ids[lane] = c + lane < s1 ? static_cast<unsigned int>(clamp_i64(id, 0, max_row)) : 0u;
     const int n = static_cast<int>(s1 - c < kWave ? s1 - c : kWave);
     for (int k = 0; k < n; k += S::U * S::R) {
       uint4 v[S::U][VPL];
@@ -337,12 +362,11 @@ using TileLdsOf = TileLds<TileShape<TT, LANES, VPL>::NB>;
 // A chunk of LANES row ids per subgroup is loaded once (one lane per id, coalesced), clamped, and
 // broadcast through the wavefront's LDS slice; each step then issues U row loads per lane.
 template <typename TT, typename OT, int LANES, int VPL, bool BUF>
-__device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLdsOf<TT, LANES, VPL>& s) {
+__device__ __forceinline__ void pool_tile(const PoolParams& p, int fi, int local_tile, TileLdsOf<TT, LANES, VPL>& s) {
   using S = Shape<TT, LANES, VPL>;
   constexpr int U = S::U;
   constexpr int R = S::R;
   constexpr int NB = TileShape<TT, LANES, VPL>::NB;
-  const int fi = tile / p.tiles_per_field;
   const char* const table = p.f[fi].table;
   const int64_t max_row = p.f[fi].max_row;
   const int64_t row_bytes = p.f[fi].row_bytes;
@@ -363,7 +387,7 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLds
   const int lane = lane_id();
   const int g = lane / LANES;   // subgroup inside the wavefront
   const int sl = lane % LANES;  // lane inside the subgroup
-  const int64_t b0 = static_cast<int64_t>(tile - fi * p.tiles_per_field) * NB;
+  const int64_t b0 = static_cast<int64_t>(local_tile) * NB;
 
   // Lane i describes bag b0 + i.
   const bool valid = lane < NB && b0 + lane < p.batch;
@@ -376,7 +400,9 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLds
   // rank among the short bags: longer first, ties by position
   const int key = shortb ? static_cast<int>(L) : -1;
   int rank = 0;
-#pragma unroll
+  // unrolled by at most 8: each unrolled readlane holds a scalar register, and 32 or 64 of them
+  // (tiles of narrow rows) would cap the wavefronts per SIMD by scalar registers
+#pragma unroll(NB < 8 ? NB : 8)
   for (int j = 0; j < NB; ++j) {
     const int kj = __builtin_amdgcn_readlane(key, j);
     rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
@@ -397,9 +423,20 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int tile, TileLds
     float acc[S::NACC];
 #pragma unroll
     for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
+#if CTI_EBAG_ID_PREFETCH
+    int64_t next_id = sl < Lb ? load_index(p, bs + sl) : 0;
+#endif
     for (int c = 0; __ballot(c < Lb) != 0; c += LANES) {
+#if CTI_EBAG_ID_PREFETCH
+      // this chunk's id was loaded one chunk ahead; the next chunk's id load is issued now, so
+      // it completes under this chunk's row loads instead of costing its own round trip
+      const int64_t id = next_id;
+      if (c + LANES + sl < Lb) next_id = load_index(p, bs + c + LANES + sl);
+#else
+      const int64_t id = c + sl < Lb ? load_index(p, bs + c + sl) : 0;
+#endif
       __syncthreads();  // orders this chunk's LDS writes after the last reads
-      s.ids[lane] = c + sl < Lb ? static_cast<unsigned int>(clamp_i64(load_index(p, bs + c + sl), 0, max_row)) : r_pad;
+      s.ids[lane] = c + sl < Lb ? static_cast<unsigned int>(clamp_i64(id, 0, max_row)) : r_pad;
       __syncthreads();
       const int live = Lb - c < LANES ? Lb - c : LANES;
       for (int k = 0; k < LANES; k += U) {
@@ -460,7 +497,37 @@ template <typename TT, typename OT, int LANES, int VPL, bool BUF>
 __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
   __shared__ TileLdsOf<TT, LANES, VPL> s;
   bin_handoff(p);
-  pool_tile<TT, OT, LANES, VPL, BUF>(p, block_tile(), s);
+  const int tile = block_tile();
+  const int fi = tile / p.tiles_per_field;
+  pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s);
+}
+
+// Main kernel of a mixed-width launch: the fields' rows differ in width but each is one lane
+// vector per lane (LANES = 1 << lanes_log2). Fields own consecutive ranges of tiles; a workgroup
+// finds its tile's field (one compare per lane and a ballot) and runs that width's tile code, so
+// fields of every width share one launch (and one binning pass and one list kernel).
+template <typename TT, typename OT, bool BUF>
+__global__ void __launch_bounds__(kMainThreads) pool_mixed_kernel(const PoolParams p) {
+  __shared__ union {
+    TileLdsOf<TT, 4, 1> l2;
+    TileLdsOf<TT, 8, 1> l3;
+    TileLdsOf<TT, 16, 1> l4;
+    TileLdsOf<TT, 32, 1> l5;
+    TileLdsOf<TT, 64, 1> l6;
+  } s;
+  bin_handoff(p);
+  const int tile = block_tile();
+  const int lane = lane_id();
+  const int first = lane < p.num_fields ? p.f[lane].tile_begin : INT32_MAX;
+  const int fi = __popcll(__ballot(first <= tile)) - 1;  // field 0 starts at tile 0
+  const int local = tile - p.f[fi].tile_begin;
+  switch (p.f[fi].lanes_log2) {
+    case 2: pool_tile<TT, OT, 4, 1, BUF>(p, fi, local, s.l2); break;
+    case 3: pool_tile<TT, OT, 8, 1, BUF>(p, fi, local, s.l3); break;
+    case 4: pool_tile<TT, OT, 16, 1, BUF>(p, fi, local, s.l4); break;
+    case 5: pool_tile<TT, OT, 32, 1, BUF>(p, fi, local, s.l5); break;
+    default: pool_tile<TT, OT, 64, 1, BUF>(p, fi, local, s.l6); break;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -564,6 +631,8 @@ __global__ void __launch_bounds__(kFusedWaves * kWave) pool_norm_kernel(const Po
     float acc[S::NACC];
 #pragma unroll
     for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
+    // No id prefetch here (unlike pool_tile): its extra registers take this kernel from 63 to 67
+    // VGPRs, one wavefront less per SIMD, and the launch from 41.9 to 49.3 us on bf16-2m.
     for (int c = 0; __ballot(c < Lb) != 0; c += LANES) {
       wave_sync();  // this chunk's LDS writes come after the last chunk's reads
       s.ids[lane] = c + sl < Lb ? static_cast<unsigned int>(clamp_i64(load_index(p, bs + c + sl), 0, max_row)) : r_pad;
@@ -665,8 +734,8 @@ __global__ void __launch_bounds__(kBinThreads) bin_kernel(const PoolParams p, Lo
   const int fi = static_cast<int>(blockIdx.y);
   const int64_t b = static_cast<int64_t>(blockIdx.x) * kBinThreads + threadIdx.x;
   bool one = false, split = false;
+  int64_t s = 0, e = 0;
   if (b < p.batch) {
-    int64_t s, e;
     bag_range(p, p.f[fi].gidx, b, s, e);
     split = e - s > p.split_threshold;
     one = !split && e - s > p.block_threshold;
@@ -693,75 +762,263 @@ __global__ void __launch_bounds__(kBinThreads) bin_kernel(const PoolParams p, Lo
   }
   const uint64_t below = (1ull << lane) - 1ull;
   const int64_t entry = (static_cast<int64_t>(fi) << 40) | b;
-  if (one) l.bags[s_base[0] + before1 + __popcll(m1 & below)] = entry;
-  if (split) l.bags[l.capacity - 1 - (s_base[1] + before2 + __popcll(m2 & below))] = entry;
+  int64_t at = -1;
+  if (one) at = s_base[0] + before1 + __popcll(m1 & below);
+  if (split) at = l.capacity - 1 - (s_base[1] + before2 + __popcll(m2 & below));
+  if (at >= 0) {
+    l.bags[at] = entry;
+    l.starts[at] = s;
+    l.ends[at] = e;
+  }
 }
 
-// List kernel: LW wavefronts per workgroup. Every bag on the split list is cut into LW contiguous
-// slices, one per wavefront, combined through LDS in wavefront order; then every bag on the
-// one-wavefront list is pooled by one wavefront (lane groups take interleaved rows).
+// Wave-uniform copy of a value every lane holds (list entries are read by all lanes alike).
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+constexpr int64_t kSampleMask = (int64_t{1} << 40) - 1;
+
+// One wavefront's share of a bag on the split list: its contiguous slice of [bs, be), partial
+// sums through LDS, combined by wavefront 0 in wavefront order. Every wavefront of the workgroup
+// calls this for the same bag.
 template <typename TT, typename OT, int LANES, int VPL, int LW>
-__global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams p, LongList l) {
+__device__ __forceinline__ void split_bag(const PoolParams& p, int fi, int64_t b, int64_t bs, int64_t be, int wave,
+                                          float* s_red, unsigned int* ids) {
   using S = Shape<TT, LANES, VPL>;
-  __shared__ float s_red[LW * S::D];
-  __shared__ unsigned int s_ids[LW * kWave];
+  const int sl = lane_id() % LANES;
+  const bool g0 = lane_id() < LANES;
+  const int64_t per = (be - bs + LW - 1) / LW;
+  const int64_t s0 = bs + wave * per < be ? bs + wave * per : be;
+  const int64_t s1 = s0 + per < be ? s0 + per : be;
+  float pa[S::NACC];
+#pragma unroll
+  for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
+  wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].row_scale, p.f[fi].max_row, p.f[fi].row_bytes, s0, s1,
+                                     pa, ids);
+  if (g0) {
+#pragma unroll
+    for (int q = 0; q < VPL; ++q) {
+#pragma unroll
+      for (int i = 0; i < S::VEC; ++i) s_red[wave * S::D + (q * LANES + sl) * S::VEC + i] = pa[q * S::VEC + i];
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && g0) {
+    float r[S::NACC];
+#pragma unroll
+    for (int q = 0; q < VPL; ++q) {
+#pragma unroll
+      for (int i = 0; i < S::VEC; ++i) {
+        const int col = (q * LANES + sl) * S::VEC + i;
+        float x = s_red[col];
+#pragma unroll
+        for (int w = 1; w < LW; ++w) x += s_red[w * S::D + col];
+        r[q * S::VEC + i] = x;
+      }
+    }
+    store_bag<TT, OT, LANES, VPL>(p, b, p.f[fi].out_col, be - bs, r);
+  }
+  __syncthreads();
+}
+
+// A bag on the one-wavefront list: the whole wavefront, lane groups taking interleaved rows.
+template <typename TT, typename OT, int LANES, int VPL>
+__device__ __forceinline__ void one_wave_bag(const PoolParams& p, int fi, int64_t b, int64_t bs, int64_t be,
+                                             unsigned int* ids) {
+  using S = Shape<TT, LANES, VPL>;
+  float pa[S::NACC];
+#pragma unroll
+  for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
+  wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].row_scale, p.f[fi].max_row, p.f[fi].row_bytes, bs, be,
+                                     pa, ids);
+  if (lane_id() < LANES) store_bag<TT, OT, LANES, VPL>(p, b, p.f[fi].out_col, be - bs, pa);
+}
+
+// Row shape of the list kernel: one shape for every field of the launch ...
+template <typename TT, typename OT, int LANES, int VPL, int LW>
+struct FixedRows {
+  static constexpr int DMAX = Shape<TT, LANES, VPL>::D;
+  __device__ static __forceinline__ void split(const PoolParams& p, int fi, int64_t b, int64_t bs, int64_t be,
+                                               int wave, float* s_red, unsigned int* ids) {
+    split_bag<TT, OT, LANES, VPL, LW>(p, fi, b, bs, be, wave, s_red, ids);
+  }
+  __device__ static __forceinline__ void one(const PoolParams& p, int fi, int64_t b, int64_t bs, int64_t be,
+                                             unsigned int* ids) {
+    one_wave_bag<TT, OT, LANES, VPL>(p, fi, b, bs, be, ids);
+  }
+};
+
+// wave_slice_partial for a row shape known only at run time: 1 << ll lanes of one vector each
+// (4 to 64 lanes), four rows in flight per lane group. Every lane holds the same registers
+// whatever the shape (one vector's accumulators), so one code path serves all shapes. Element
+// order and the combine's order equal wave_slice_partial<TT, 1 << ll, 1>, so results do too.
+template <typename TT>
+__device__ __forceinline__ void wave_slice_partial_rt(const PoolParams& p, int fi, int ll, int64_t s0, int64_t s1,
+                                                      float* pa, unsigned int* ids) {
+  constexpr int VB = Elem<TT>::kVecBytes;
+  constexpr int VEC = VB / Elem<TT>::kBytes;
+  constexpr int U = 4;
+  const char* const table = p.f[fi].table;
+  const float* const row_scale = p.f[fi].row_scale;
+  const int64_t max_row = p.f[fi].max_row;
+  const int64_t row_bytes = p.f[fi].row_bytes;
   const int lane = lane_id();
-  const int wave = static_cast<int>(threadIdx.x) >> 6;
-  const int g = lane / LANES, sl = lane % LANES;
-  const unsigned int n = __hip_atomic_load(l.total2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (unsigned int j = blockIdx.x; j < n; j += gridDim.x) {
-    const int64_t item = l.bags[l.capacity - 1 - j];
-    const int fi = static_cast<int>(item >> 40);
-    const int64_t b = item & ((int64_t{1} << 40) - 1);
-    int64_t bs, be;
-    bag_range(p, p.f[fi].gidx, b, bs, be);
+  const int R = kWave >> ll;  // lane groups; U * R divides 64, so every row slot e below is < 64
+  const int g = lane >> ll, sl = lane & ((1 << ll) - 1);
+#if CTI_EBAG_ID_PREFETCH
+  int64_t next_id = s0 + lane < s1 ? load_index(p, s0 + lane) : 0;
+#endif
+  for (int64_t c = s0; c < s1; c += kWave) {
+#if CTI_EBAG_ID_PREFETCH
+    const int64_t id = next_id;
+    if (c + kWave + lane < s1) next_id = load_index(p, c + kWave + lane);
+#else
+    const int64_t id = c + lane < s1 ? load_index(p, c + lane) : 0;
+#endif
+    ids[lane] = c + lane < s1 ? static_cast<unsigned int>(clamp_i64(id, 0, max_row)) : 0u;
+    const int n = static_cast<int>(s1 - c < kWave ? s1 - c : kWave);
+    for (int k = 0; k < n; k += U * R) {
+      uint4 v[U];
+      float sc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = k + u * R + g;
+        const char* row = table + static_cast<uint64_t>(ids[e]) * static_cast<uint64_t>(row_bytes);
+        const bool act = e < n;
+        v[u] = act ? load_row_vec<TT>(row + sl * VB) : make_uint4(0u, 0u, 0u, 0u);
+        sc[u] = 1.f;
+        if constexpr (Quantized<TT>::value) sc[u] = act ? row_scale[ids[e]] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc_row<TT>(pa, v[u], sc[u]);
+    }
+  }
+  for (int mk = 1 << ll; mk < kWave; mk <<= 1) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) pa[i] += shfl_xor_f32(pa[i], mk);
+  }
+}
+
+template <typename TT, typename OT>
+__device__ __forceinline__ void store_bag_rt(const PoolParams& p, int64_t b, int out_col, int64_t L, int sl,
+                                             const float* a) {
+  constexpr int VEC = Elem<TT>::kVecBytes / Elem<TT>::kBytes;
+  float r[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) r[i] = a[i];
+  if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<VEC>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
+  store_out<VEC>(reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col + sl * VEC, r);
+}
+
+// ... or, in a mixed launch, each field's own (one lane vector per lane, 1 << lanes_log2 lanes
+// per row, kMixedLo <= lanes_log2 <= kMixedHi), chosen at run time.
+template <typename TT, typename OT, int LW>
+struct MixedRows {
+  static constexpr int VEC = Elem<TT>::kVecBytes / Elem<TT>::kBytes;
+  static constexpr int DMAX = Shape<TT, 1 << kMixedHi, 1>::D;
+  __device__ static __forceinline__ void split(const PoolParams& p, int fi, int64_t b, int64_t bs, int64_t be,
+                                               int wave, float* s_red, unsigned int* ids) {
+    const int ll = p.f[fi].lanes_log2;
+    const int D = VEC << ll;
+    const int sl = lane_id() & ((1 << ll) - 1);
+    const bool g0 = lane_id() < (1 << ll);
     const int64_t per = (be - bs + LW - 1) / LW;
     const int64_t s0 = bs + wave * per < be ? bs + wave * per : be;
     const int64_t s1 = s0 + per < be ? s0 + per : be;
-    float pa[S::NACC];
+    float pa[VEC];
 #pragma unroll
-    for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
-    wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].row_scale, p.f[fi].max_row, p.f[fi].row_bytes, s0,
-                                       s1, pa, s_ids + wave * kWave);
-    if (g == 0) {
+    for (int i = 0; i < VEC; ++i) pa[i] = 0.f;
+    wave_slice_partial_rt<TT>(p, fi, ll, s0, s1, pa, ids);
+    if (g0) {
 #pragma unroll
-      for (int q = 0; q < VPL; ++q) {
-#pragma unroll
-        for (int i = 0; i < S::VEC; ++i) s_red[wave * S::D + (q * LANES + sl) * S::VEC + i] = pa[q * S::VEC + i];
-      }
+      for (int i = 0; i < VEC; ++i) s_red[wave * D + sl * VEC + i] = pa[i];
     }
     __syncthreads();
-    if (wave == 0 && g == 0) {
-      float r[S::NACC];
+    if (wave == 0 && g0) {
+      float r[VEC];
 #pragma unroll
-      for (int q = 0; q < VPL; ++q) {
+      for (int i = 0; i < VEC; ++i) {
+        float x = s_red[sl * VEC + i];
 #pragma unroll
-        for (int i = 0; i < S::VEC; ++i) {
-          const int col = (q * LANES + sl) * S::VEC + i;
-          float x = s_red[col];
-#pragma unroll
-          for (int w = 1; w < LW; ++w) x += s_red[w * S::D + col];
-          r[q * S::VEC + i] = x;
-        }
+        for (int w = 1; w < LW; ++w) x += s_red[w * D + sl * VEC + i];
+        r[i] = x;
       }
-      store_bag<TT, OT, LANES, VPL>(p, b, p.f[fi].out_col, be - bs, r);
+      store_bag_rt<TT, OT>(p, b, p.f[fi].out_col, be - bs, sl, r);
     }
     __syncthreads();
   }
+  __device__ static __forceinline__ void one(const PoolParams& p, int fi, int64_t b, int64_t bs, int64_t be,
+                                             unsigned int* ids) {
+    const int ll = p.f[fi].lanes_log2;
+    float pa[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) pa[i] = 0.f;
+    wave_slice_partial_rt<TT>(p, fi, ll, bs, be, pa, ids);
+    if (lane_id() < (1 << ll)) store_bag_rt<TT, OT>(p, b, p.f[fi].out_col, be - bs, lane_id(), pa);
+  }
+};
+
+// List kernel: LW wavefronts per workgroup. Every bag on the split list is cut into LW contiguous
+// slices, one per wavefront, combined through LDS in wavefront order; then every bag on the
+// one-wavefront list is pooled by one wavefront (lane groups take interleaved rows). List entries
+// carry their bag's range, and the entry of a wavefront's next bag is loaded while it pools the
+// current one, so a bag costs no lookup round trip of its own.
+template <typename TT, typename OT, int LW, typename Rows>
+__global__ void __launch_bounds__(LW * kWave) pool_long_kernel(const PoolParams p, LongList l) {
+  __shared__ float s_red[LW * Rows::DMAX];
+  __shared__ unsigned int s_ids[LW * kWave];
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  unsigned int* const ids = s_ids + wave * kWave;
+
+  const unsigned int n = __hip_atomic_load(l.total2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int64_t item = 0, bs = 0, be = 0;
+  if (blockIdx.x < n) {
+    const int64_t at = l.capacity - 1 - blockIdx.x;
+    item = l.bags[at];
+    bs = l.starts[at];
+    be = l.ends[at];
+  }
+  for (unsigned int j = blockIdx.x; j < n; j += gridDim.x) {
+    const unsigned int jn = j + gridDim.x;
+    int64_t item_n = 0, bs_n = 0, be_n = 0;
+    if (jn < n) {  // the next bag's entry, in flight while this one is pooled
+      const int64_t at = l.capacity - 1 - jn;
+      item_n = l.bags[at];
+      bs_n = l.starts[at];
+      be_n = l.ends[at];
+    }
+    const int64_t it = uniform_i64(item);
+    Rows::split(p, static_cast<int>(it >> 40), it & kSampleMask, uniform_i64(bs), uniform_i64(be), wave, s_red, ids);
+    item = item_n;
+    bs = bs_n;
+    be = be_n;
+  }
+
   const unsigned int n1 = __hip_atomic_load(l.total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const unsigned int stride = gridDim.x * LW;
-  for (unsigned int j = blockIdx.x * LW + static_cast<unsigned int>(wave); j < n1; j += stride) {
-    const int64_t item = l.bags[j];
-    const int fi = static_cast<int>(item >> 40);
-    const int64_t b = item & ((int64_t{1} << 40) - 1);
-    int64_t bs, be;
-    bag_range(p, p.f[fi].gidx, b, bs, be);
-    float pa[S::NACC];
-#pragma unroll
-    for (int i = 0; i < S::NACC; ++i) pa[i] = 0.f;
-    wave_slice_partial<TT, LANES, VPL>(p, p.f[fi].table, p.f[fi].row_scale, p.f[fi].max_row, p.f[fi].row_bytes, bs,
-                                       be, pa, s_ids + wave * kWave);
-    if (g == 0) store_bag<TT, OT, LANES, VPL>(p, b, p.f[fi].out_col, be - bs, pa);
+  unsigned int j = blockIdx.x * LW + static_cast<unsigned int>(wave);
+  if (j < n1) {
+    item = l.bags[j];
+    bs = l.starts[j];
+    be = l.ends[j];
+  }
+  for (; j < n1; j += stride) {
+    const unsigned int jn = j + stride;
+    int64_t item_n = 0, bs_n = 0, be_n = 0;
+    if (jn < n1) {
+      item_n = l.bags[jn];
+      bs_n = l.starts[jn];
+      be_n = l.ends[jn];
+    }
+    const int64_t it = uniform_i64(item);
+    Rows::one(p, static_cast<int>(it >> 40), it & kSampleMask, uniform_i64(bs), uniform_i64(be), ids);
+    item = item_n;
+    bs = bs_n;
+    be = be_n;
   }
 }
 
@@ -867,25 +1124,48 @@ int pick_variant(const cti_ebag_table& t, int tb, int ob, const void* out, int64
   return kVarGeneric;
 }
 
+void launch_bins(const PoolParams& p, const LongList& l, hipStream_t s) {
+  const dim3 bgrid(static_cast<unsigned>((p.batch + kBinThreads - 1) / kBinThreads), static_cast<unsigned>(p.num_fields));
+  hipLaunchKernelGGL(bin_kernel, bgrid, dim3(kBinThreads), 0, s, p, l);
+}
+
+// Workgroups of the list kernel: at most min(bags, nnz / (block_threshold + 1)) bags can be
+// listed, and the workgroups loop over the list.
+unsigned list_blocks(const PoolParams& p) {
+  int64_t most = p.nnz / (p.block_threshold + 1) + 1;
+  const int64_t bags = p.batch * p.num_fields;
+  if (most > bags) most = bags;
+  return static_cast<unsigned>(most < kLongBlocksMax ? (most > 0 ? most : 1) : kLongBlocksMax);
+}
+
 template <typename TT, typename OT, int LANES, int VPL>
 void launch_shape(const PoolParams& p, const LongList* l, hipStream_t s) {
-  if (l) {
-    const dim3 bgrid(static_cast<unsigned>((p.batch + kBinThreads - 1) / kBinThreads), static_cast<unsigned>(p.num_fields));
-    hipLaunchKernelGGL(bin_kernel, bgrid, dim3(kBinThreads), 0, s, p, *l);
-  }
-const dim3 grid(static_cast<unsigned>(p.num_tiles)), block(kMainThreads);
+  if (l) launch_bins(p, *l, s);
+  const dim3 grid(static_cast<unsigned>(p.num_tiles)), block(kMainThreads);
   if (p.buffer_ok)
     hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true>), grid, block, 0, s, p);
   else
     hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, false>), grid, block, 0, s, p);
   if (l) {
     constexpr int LW = VPL >= 4 ? 4 : 8;  // keeps the LDS partials at <= 32 KB
-    // at most min(bags, nnz / (block_threshold + 1)) bags can be listed
-    int64_t most = p.nnz / (p.block_threshold + 1) + 1;
-    const int64_t bags = p.batch * p.num_fields;
-    if (most > bags) most = bags;
-    const unsigned blocks = static_cast<unsigned>(most < kLongBlocksMax ? (most > 0 ? most : 1) : kLongBlocksMax);
-    hipLaunchKernelGGL((pool_long_kernel<TT, OT, LANES, VPL, LW>), dim3(blocks), dim3(LW * kWave), 0, s, p, *l);
+    hipLaunchKernelGGL((pool_long_kernel<TT, OT, LW, FixedRows<TT, OT, LANES, VPL, LW>>), dim3(list_blocks(p)),
+                       dim3(LW * kWave), 0, s, p, *l);
+  }
+}
+
+// A mixed-width launch: fields of several one-vector-per-lane row shapes in one sequence.
+template <typename TT, typename OT>
+void launch_mixed(const PoolParams& p, const LongList* l, hipStream_t s) {
+  if (l) launch_bins(p, *l, s);
+  const dim3 grid(static_cast<unsigned>(p.num_tiles)), block(kMainThreads);
+  if (p.buffer_ok)
+    hipLaunchKernelGGL((pool_mixed_kernel<TT, OT, true>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((pool_mixed_kernel<TT, OT, false>), grid, block, 0, s, p);
+  if (l) {
+    constexpr int LW = 8;
+    hipLaunchKernelGGL((pool_long_kernel<TT, OT, LW, MixedRows<TT, OT, LW>>), dim3(list_blocks(p)), dim3(LW * kWave), 0,
+                       s, p, *l);
   }
 }
 
@@ -901,6 +1181,7 @@ hipError_t launch_variant(int variant, const PoolParams& p, const LongList* l, h
     case 6: launch_shape<TT, OT, 64, 1>(p, l, s); break;
     case kVarL64V2: launch_shape<TT, OT, 64, 2>(p, l, s); break;
     case kVarL64V4: launch_shape<TT, OT, 64, 4>(p, l, s); break;
+    case kVarMixed: launch_mixed<TT, OT>(p, l, s); break;
     default:
       hipLaunchKernelGGL((pool_generic_kernel<TT, OT>), dim3(static_cast<unsigned>(p.num_tiles)), dim3(kMainThreads), 0, s, p);
       break;
@@ -978,15 +1259,36 @@ int run_job(const Job& j, hipStream_t stream) {
     list.total = reinterpret_cast<unsigned int*>(ws) + 1;
     list.count2 = reinterpret_cast<unsigned int*>(ws) + 2;
     list.total2 = reinterpret_cast<unsigned int*>(ws) + 3;
+    list.capacity = (workspace_bytes(j.batch, j.num_fields) - kWorkspaceHeader) / 24;
     list.bags = reinterpret_cast<int64_t*>(ws + kWorkspaceHeader);
-    list.capacity = (workspace_bytes(j.batch, j.num_fields) - kWorkspaceHeader) / 8;
+    list.starts = list.bags + list.capacity;
+    list.ends = list.starts + list.capacity;
   }
-  // Group fields by kernel variant; each group is one launch sequence (per 64 fields).
+  // Group fields by kernel variant; each group is one launch sequence (per 64 fields). Fields
+  // whose rows are one lane vector per lane but of different widths form one mixed group.
   std::vector<int> var(j.num_fields);
   for (int f = 0; f < j.num_fields; ++f) var[f] = pick_variant(j.tables[f], tb, ob, j.out, j.out_row_stride);
-  for (int v = 0; v < kNumVariants; ++v) {
+  int one_vec_shapes = 0;
+  for (int v = kMixedLo; v <= kMixedHi; ++v) {
+    for (int f = 0; f < j.num_fields; ++f) {
+      if (var[f] == v) {
+        ++one_vec_shapes;
+        break;
+      }
+    }
+  }
+  const bool mixed = one_vec_shapes > 1;
+  for (int v = 0; v <= kVarMixed; ++v) {
     std::vector<int> fields;
-    for (int f = 0; f < j.num_fields; ++f) if (var[f] == v) fields.push_back(f);
+    if (v == kVarMixed) {
+      if (!mixed) continue;
+      // widest rows first (fewest bags per tile), so those tiles start first
+      for (int w = kMixedHi; w >= kMixedLo; --w)
+        for (int f = 0; f < j.num_fields; ++f) if (var[f] == w) fields.push_back(f);
+    } else {
+      if (mixed && v >= kMixedLo && v <= kMixedHi) continue;
+      for (int f = 0; f < j.num_fields; ++f) if (var[f] == v) fields.push_back(f);
+    }
     for (size_t c0 = 0; c0 < fields.size(); c0 += kMaxFields) {
       PoolParams p;
       memset(&p, 0, sizeof(p));
@@ -1013,17 +1315,18 @@ int run_job(const Job& j, hipStream_t stream) {
       if (v != kVarGeneric && p.sub_threshold > kMaxShortBag) p.sub_threshold = kMaxShortBag;
       p.bin_count = bins ? list.count : nullptr;
       p.bin_total = bins ? list.total : nullptr;
-      const int bpt = bags_per_tile(v);
-      const int64_t tiles_per_field = (j.batch + bpt - 1) / bpt;
       const size_t nf = fields.size() - c0 < static_cast<size_t>(kMaxFields) ? fields.size() - c0 : kMaxFields;
-      if (tiles_per_field * static_cast<int64_t>(nf) > INT32_MAX)
-        return set_error(CTI_EBAG_EUNSUPPORTED, "batch of %lld samples needs more than 2^31 tiles", (long long)j.batch);
       p.num_fields = static_cast<int32_t>(nf);
       bool all_buf = true;
+      int64_t tiles = 0;
       for (size_t i = 0; i < nf; ++i) {
         const int f = fields[c0 + i];
         const cti_ebag_table& t = j.tables[f];
         FieldDesc& d = p.f[i];
+        const int bpt = bags_per_tile(var[f]);
+        d.lanes_log2 = var[f] <= 6 ? var[f] : 0;
+        d.tile_begin = static_cast<int32_t>(tiles < INT32_MAX ? tiles : INT32_MAX);
+        tiles += (j.batch + bpt - 1) / bpt;
         d.table = static_cast<const char*>(t.data);
         d.row_scale = j.tdt == CTI_EBAG_I8 ? t.row_scale : nullptr;
         d.max_row = t.rows - 1;
@@ -1039,9 +1342,12 @@ int run_job(const Job& j, hipStream_t stream) {
         d.span_bytes = pow2 && fits ? static_cast<uint32_t>(span) : 0u;
         all_buf = all_buf && d.span_bytes != 0;
       }
+      if (tiles > INT32_MAX)
+        return set_error(CTI_EBAG_EUNSUPPORTED, "batch of %lld samples needs more than 2^31 tiles", (long long)j.batch);
       p.buffer_ok = all_buf ? 1 : 0;
-      p.num_tiles = static_cast<int32_t>(tiles_per_field * static_cast<int64_t>(nf));
-      p.tiles_per_field = static_cast<int32_t>(tiles_per_field);
+      p.num_tiles = static_cast<int32_t>(tiles);
+      // every field of a single-shape launch has the same number of tiles
+      p.tiles_per_field = static_cast<int32_t>(tiles / static_cast<int64_t>(nf));
       const hipError_t e = launch_typed(j.tdt, j.odt, v, p, bins ? &list : nullptr, stream);
       if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "pooling kernel launch failed: %s", hipGetErrorString(e));
     }
@@ -1051,9 +1357,10 @@ int run_job(const Job& j, hipStream_t stream) {
 
 bool dtype_ok(int32_t dt) { return dt == CTI_EBAG_F32 || dt == CTI_EBAG_BF16 || dt == CTI_EBAG_F16; }
 
+// Header, then three arrays of one entry per bag of a launch (field / sample, start, end).
 int64_t workspace_bytes(int64_t batch, int32_t num_fields) {
   const int64_t per_launch = num_fields < kMaxFields ? num_fields : kMaxFields;
-  return kWorkspaceHeader + 8 * batch * per_launch;
+  return kWorkspaceHeader + 24 * batch * per_launch;
 }
 
 }  // namespace

@@ -151,7 +151,8 @@ int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const 
                      const cti_ebag_options* opts, void* stream);
 
 /* Bytes of device workspace cti_ebag_forward needs with opts->use_bins = 1
- * (256 + 8 * batch_size * min(num_fields, 64)); -1 for negative arguments. */
+ * (256 + 24 * batch_size * min(num_fields, 64): list counters, then the field / sample and the
+ * value range of each listed bag); -1 for negative arguments. */
 int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fields);
 
 /*

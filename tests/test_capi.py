@@ -154,8 +154,8 @@ def test_pack_and_merge_reject_bad_arguments(pkg):
 
 def test_workspace_query(pkg):
     lib = pkg._capi.lib()
-    assert lib.cti_ebag_workspace_bytes(4096, 28) == 256 + 8 * 4096 * 28
-    assert lib.cti_ebag_workspace_bytes(10, 100) == 256 + 8 * 10 * 64
+    assert lib.cti_ebag_workspace_bytes(4096, 28) == 256 + 24 * 4096 * 28
+    assert lib.cti_ebag_workspace_bytes(10, 100) == 256 + 24 * 10 * 64
     assert lib.cti_ebag_workspace_bytes(-1, 28) < 0
 
 
