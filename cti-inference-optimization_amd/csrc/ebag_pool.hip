@@ -32,10 +32,16 @@
 //     fp32 division except for quotients below the normal range (those take the division).
 //     Conversions to bf16 use the hardware round-to-nearest-even pack.
 //   * Length-binning pass (optional): one thread per bag; bags longer than block_threshold are
-//     appended to a list in the caller's workspace (one atomic per wavefront).
-//   * Long kernel: 8 wavefronts (4 for 2 KB rows) per workgroup, looping over the list; each bag
-//     is cut into one contiguous slice per wavefront, and the wavefront partials are combined
-//     through LDS in wavefront order.
+//     appended, with their value ranges, to one of two lists in the caller's workspace (one
+//     global atomic per workgroup and list): up to split_threshold rows on the one-wavefront
+//     list, longer ones on the split list.
+//   * Long kernel: 8 wavefronts (4 for 2 KB rows) per workgroup, looping over the lists; a bag on
+//     the split list is cut into one contiguous slice per wavefront and the wavefront partials
+//     are combined through LDS in wavefront order; a bag on the one-wavefront list is pooled by
+//     one wavefront, which loads its next bag's entry meanwhile.
+//   * Fields whose rows differ in width but are 4 to 64 lanes of one vector share one launch
+//     sequence: the main kernel runs each tile's own row shape, the long kernel picks each bag's
+//     shape at run time.
 //   * List counter hand-off without contended atomics: the binning pass counts into `count`; the
 //     main kernel, which runs between the two, has one thread move `count` to `total` and zero
 //     `count`; the long kernel reads `total`. A call therefore leaves `count` at zero for the next.
