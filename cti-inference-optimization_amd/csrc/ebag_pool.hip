@@ -146,7 +146,6 @@ struct PoolParams {
   int64_t split_threshold;  // listed bags longer than this are split over a workgroup
   unsigned int* bin_count;  // binning: list lengths being built (NULL without binning): [0] one-wave, [2] split
   unsigned int* bin_total;  // binning: list lengths handed to the list kernel: [0] one-wave, [2] split
-  const int32_t* tile_order;  // optional dispatch order (order_kernel's layout), NULL = tile order
   int32_t num_fields;
   int32_t num_tiles;
   int32_t tiles_per_field;  // every field of a launch has the same number of tiles
@@ -409,8 +408,7 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int fi, int local
   int rank = 0;
   // unrolled by at most 8: each unrolled readlane holds a scalar register, and 32 or 64 of them
   // (tiles of narrow rows) would cap the wavefronts per SIMD by scalar registers
-  constexpr int kRankUnroll = NB < 8 ? NB : 8;
-#pragma unroll kRankUnroll
+#pragma unroll(NB < 8 ? NB : 8)
   for (int j = 0; j < NB; ++j) {
     const int kj = __builtin_amdgcn_readlane(key, j);
     rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
@@ -500,89 +498,12 @@ __device__ __forceinline__ void bin_handoff(const PoolParams& p) {
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// Dispatch order. Workgroups are dealt to the XCDs round-robin and block_tile() gives XCD x a
-// contiguous range of dispatch positions, which it starts in order as wavefront slots free up.
-// A launch ends with a drain: tiles whose bags are long, started late, run on while the rest of
-// the chip idles. An order that starts each XCD's tiles with the most rows first removes most of
-// that drain (bf16-2m: 36.2-36.8 us instead of 40.3-41.6). order_kernel computes such an order
-// for a batch; a later launch of the same shape reads it. Each XCD keeps its own set of tiles
-// (only their sequence changes), so per-XCD cache locality is unchanged, and each output row
-// still has one writer, so results do not depend on the order.
-//
-// Order buffer (int32): [0] tiles of the launch it was made for, [1] kOrderMagic, [2..3] unused,
-// [4 + position] = tile. The host checks the buffer holds 4 + num_tiles entries; the main kernel
-// uses the order only if [0] and [1] match its launch, and takes its own position for any entry
-// outside the launch's tiles, so no order can make it read or write out of bounds.
-constexpr int32_t kOrderMagic = 0x4f524452;
-constexpr int kOrderHeader = 4;
-constexpr int kOrderThreads = 256;
-constexpr int kOrderBuckets = 64;
-
-__device__ __forceinline__ int ordered_tile(const PoolParams& p, int pos) {
-  if (!p.tile_order) return pos;
-  if (p.tile_order[0] != p.num_tiles || p.tile_order[1] != kOrderMagic) return pos;
-  const int t = p.tile_order[kOrderHeader + pos];
-  return t >= 0 && t < p.num_tiles ? t : pos;
-}
-
-// Rows of tile t (NB consecutive bags of one field), from the offsets alone.
-__device__ __forceinline__ int64_t tile_rows(const PoolParams& p, int t, int nb) {
-  const int fi = t / p.tiles_per_field;
-  const int64_t b0 = static_cast<int64_t>(t - fi * p.tiles_per_field) * nb;
-  const int64_t b1 = b0 + nb < p.batch ? b0 + nb : p.batch;
-  if (b0 >= b1) return 0;
-  const int64_t i = static_cast<int64_t>(p.f[fi].gidx) * p.offsets_stride;
-  return load_offset(p, p.offsets, i + b1) - load_offset(p, p.offsets, i + b0);  // val_base cancels
-}
-
-// One workgroup per XCD range: a counting sort of the range's tiles by rows per bag (64 buckets,
-// most rows first; the order inside a bucket is whatever the LDS atomics give).
-__global__ void __launch_bounds__(kOrderThreads) order_kernel(const PoolParams p, int32_t* order, int nb) {
-  __shared__ unsigned int s_count[kOrderBuckets];
-  __shared__ int s_next[kOrderBuckets];
-  const int n = p.num_tiles;
-  const int x = static_cast<int>(blockIdx.x);  // XCD range 0..7
-  const int q = n >> 3, r = n & 7;
-  const int lo = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
-  const int cnt = q + (x < r ? 1 : 0);
-  const int tid = static_cast<int>(threadIdx.x);
-  auto bucket = [&](int t) {
-    int64_t per_bag = tile_rows(p, t, nb) / nb;
-    per_bag = per_bag < 0 ? 0 : (per_bag > kOrderBuckets - 1 ? kOrderBuckets - 1 : per_bag);
-    return kOrderBuckets - 1 - static_cast<int>(per_bag);  // most rows first
-  };
-  for (int i = tid; i < kOrderBuckets; i += kOrderThreads) s_count[i] = 0u;
-  __syncthreads();
-  for (int k = tid; k < cnt; k += kOrderThreads) atomicAdd(&s_count[bucket(lo + k)], 1u);
-  __syncthreads();
-  if (tid == 0) {
-    int at = lo;
-    for (int b = 0; b < kOrderBuckets; ++b) {
-      s_next[b] = at;
-      at += static_cast<int>(s_count[b]);
-    }
-  }
-  __syncthreads();
-  for (int k = tid; k < cnt; k += kOrderThreads) {
-    const int t = lo + k;
-    const int at = atomicAdd(&s_next[bucket(t)], 1);  // lands in [lo, lo + cnt)
-    order[kOrderHeader + at] = t;
-  }
-  if (x == 0 && tid == 0) {
-    order[0] = n;
-    order[1] = kOrderMagic;
-    order[2] = 0;
-    order[3] = 0;
-  }
-}
-
 // Main kernel: one wavefront per workgroup, one tile per workgroup.
 template <typename TT, typename OT, int LANES, int VPL, bool BUF>
 __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
   __shared__ TileLdsOf<TT, LANES, VPL> s;
   bin_handoff(p);
-  const int tile = ordered_tile(p, block_tile());
+  const int tile = block_tile();
   const int fi = tile / p.tiles_per_field;
   pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s);
 }
@@ -1312,10 +1233,6 @@ struct Job {
   int32_t block_threshold;  // 0 = default (with bins)
   int32_t split_threshold;  // 0 = default (with bins)
   void* workspace;
-  const int32_t* tile_order;  // optional dispatch order for the main kernel (see order_kernel)
-  int64_t tile_order_bytes;
-  int32_t* make_order;        // set: compute the dispatch order into this buffer instead of pooling
-  int64_t make_order_bytes;
 };
 
 int validate_tables(const Job& j) {
@@ -1367,7 +1284,6 @@ int run_job(const Job& j, hipStream_t stream) {
     }
   }
   const bool mixed = one_vec_shapes > 1;
-  std::vector<std::pair<int, PoolParams>> launches;  // (variant, parameters) in launch order
   for (int v = 0; v <= kVarMixed; ++v) {
     std::vector<int> fields;
     if (v == kVarMixed) {
@@ -1438,36 +1354,9 @@ int run_job(const Job& j, hipStream_t stream) {
       p.num_tiles = static_cast<int32_t>(tiles);
       // every field of a single-shape launch has the same number of tiles
       p.tiles_per_field = static_cast<int32_t>(tiles / static_cast<int64_t>(nf));
-      launches.push_back({v, p});
+      const hipError_t e = launch_typed(j.tdt, j.odt, v, p, bins ? &list : nullptr, stream);
+      if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "pooling kernel launch failed: %s", hipGetErrorString(e));
     }
-  }
-  // A dispatch order applies to a job that is one main-kernel launch of one row shape.
-  const bool orderable = launches.size() == 1 && launches[0].first != kVarGeneric && launches[0].first != kVarMixed;
-  if (j.make_order) {
-    if (!orderable)
-      return set_error(CTI_EBAG_EUNSUPPORTED, "a dispatch order needs a job of one row shape and at most %d fields",
-                       kMaxFields);
-    const PoolParams& p = launches[0].second;
-    if (j.make_order_bytes < (kOrderHeader + static_cast<int64_t>(p.num_tiles)) * 4)
-      return set_error(CTI_EBAG_EINVAL, "order buffer of %lld bytes; this job needs %lld", (long long)j.make_order_bytes,
-                       (long long)((kOrderHeader + static_cast<int64_t>(p.num_tiles)) * 4));
-    hipLaunchKernelGGL(order_kernel, dim3(8), dim3(kOrderThreads), 0, stream, p, j.make_order,
-                       bags_per_tile(launches[0].first));
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "order kernel launch failed: %s", hipGetErrorString(e));
-    return CTI_EBAG_OK;
-  }
-  if (j.tile_order && orderable) {
-    PoolParams& p = launches[0].second;
-    if (j.tile_order_bytes < (kOrderHeader + static_cast<int64_t>(p.num_tiles)) * 4)
-      return set_error(CTI_EBAG_EINVAL, "tile order of %lld bytes; this job's launch needs %lld",
-                       (long long)j.tile_order_bytes, (long long)((kOrderHeader + static_cast<int64_t>(p.num_tiles)) * 4));
-    p.tile_order = j.tile_order;
-  }
-  for (const auto& l : launches) {
-    const bool bins = j.use_bins && l.first != kVarGeneric;
-    const hipError_t e = launch_typed(j.tdt, j.odt, l.first, l.second, bins ? &list : nullptr, stream);
-    if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "pooling kernel launch failed: %s", hipGetErrorString(e));
   }
   return CTI_EBAG_OK;
 }
@@ -1718,15 +1607,12 @@ extern "C" int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fiel
   return workspace_bytes(batch_size, num_fields);
 }
 
-namespace cti {
-namespace {
-
-// Checks the arguments cti_ebag_forward and cti_ebag_tile_order share and fills `j` from them.
-// `empty` is set for a zero-sized call (nothing to launch).
-int make_job(Job& j, bool& empty, const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
-             int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables, int32_t table_dtype,
-             int32_t pooling, void* out, int32_t out_dtype, int64_t out_row_stride) {
-  empty = false;
+extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
+                                int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables,
+                                int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
+                                int64_t out_row_stride, void* workspace, int64_t workspace_bytes_given,
+                                const cti_ebag_options* opts, void* stream) {
+  clear_error();
   if (index_type != CTI_EBAG_I64 && index_type != CTI_EBAG_I32)
     return set_error(CTI_EBAG_EINVAL, "unknown index type code %d", index_type);
   if (!dtype_ok(table_dtype) && table_dtype != CTI_EBAG_I8)
@@ -1737,13 +1623,11 @@ int make_job(Job& j, bool& empty, const void* values, int32_t index_type, int64_
   if (batch_size < 0) return set_error(CTI_EBAG_EINVAL, "batch_size must be >= 0 (got %lld)", (long long)batch_size);
   if (num_fields < 0) return set_error(CTI_EBAG_EINVAL, "num_fields must be >= 0 (got %d)", num_fields);
   if (out_row_stride < 1) return set_error(CTI_EBAG_EINVAL, "out_row_stride must be >= 1 (got %lld)", (long long)out_row_stride);
-  if (batch_size == 0 || num_fields == 0) {
-    empty = true;
-    return CTI_EBAG_OK;
-  }
+  if (batch_size == 0 || num_fields == 0) return CTI_EBAG_OK;
   if (!tables) return set_error(CTI_EBAG_EINVAL, "tables (host array) is NULL");
   if (!offsets || !out || (nnz > 0 && !values)) return set_error(CTI_EBAG_EINVAL, "NULL device pointer among values/offsets/out");
   if (batch_size >= (int64_t{1} << 40)) return set_error(CTI_EBAG_EUNSUPPORTED, "batch_size must be < 2^40");
+  Job j;
   memset(&j, 0, sizeof(j));
   j.values = values;
   j.idx32 = index_type == CTI_EBAG_I32;
@@ -1759,36 +1643,12 @@ int make_job(Job& j, bool& empty, const void* values, int32_t index_type, int64_
   j.out = out;
   j.odt = out_dtype;
   j.out_row_stride = out_row_stride;
-  return validate_tables(j);
-}
-
-int64_t tile_order_bytes(int64_t batch, int32_t num_fields) {
-  const int64_t per_launch = num_fields < kMaxFields ? num_fields : kMaxFields;
-  return (kOrderHeader + batch * per_launch) * 4;  // one bag per tile at most
-}
-
-}  // namespace
-}  // namespace cti
-
-extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
-                                int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables,
-                                int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
-                                int64_t out_row_stride, void* workspace, int64_t workspace_bytes_given,
-                                const cti_ebag_options* opts, void* stream) {
-  clear_error();
-  Job j;
-  bool empty;
-  int rc = make_job(j, empty, values, index_type, nnz, offsets, batch_size, num_fields, tables, table_dtype, pooling,
-                    out, out_dtype, out_row_stride);
-  if (rc != CTI_EBAG_OK || empty) return rc;
   j.workspace = workspace;
   if (opts) {
     j.sub_threshold = opts->long_threshold;
     j.use_bins = opts->use_bins != 0;
     j.block_threshold = opts->block_threshold;
     j.split_threshold = opts->split_threshold;
-    j.tile_order = opts->tile_order;
-    j.tile_order_bytes = opts->tile_order_bytes;
   }
   if (j.use_bins) {
     const int64_t need = workspace_bytes(batch_size, num_fields);
@@ -1798,29 +1658,7 @@ extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t 
     if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
       return set_error(CTI_EBAG_EINVAL, "workspace must be 256-byte aligned");
   }
-  if (j.tile_order && reinterpret_cast<uintptr_t>(j.tile_order) % 4 != 0)
-    return set_error(CTI_EBAG_EINVAL, "tile_order must be 4-byte aligned");
+  const int rc = validate_tables(j);
+  if (rc != CTI_EBAG_OK) return rc;
   return run_job(j, static_cast<hipStream_t>(stream));
-}
-
-extern "C" int cti_ebag_tile_order(const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
-                                   int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables,
-                                   int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
-                                   int64_t out_row_stride, int32_t* order, int64_t order_bytes, void* stream) {
-  clear_error();
-  Job j;
-  bool empty;
-  int rc = make_job(j, empty, values, index_type, nnz, offsets, batch_size, num_fields, tables, table_dtype, pooling,
-                    out, out_dtype, out_row_stride);
-  if (rc != CTI_EBAG_OK || empty) return rc;
-  if (!order) return set_error(CTI_EBAG_EINVAL, "order buffer is NULL");
-  if (reinterpret_cast<uintptr_t>(order) % 4 != 0) return set_error(CTI_EBAG_EINVAL, "order must be 4-byte aligned");
-  j.make_order = order;
-  j.make_order_bytes = order_bytes;
-  return run_job(j, static_cast<hipStream_t>(stream));
-}
-
-extern "C" int64_t cti_ebag_tile_order_bytes(int64_t batch_size, int32_t num_fields) {
-  if (batch_size < 0 || num_fields < 0) return -1;
-  return tile_order_bytes(batch_size, num_fields);
 }

@@ -436,12 +436,6 @@ class PooledEmbedding:
     ``plan(values, offsets, out=None)`` pools one batch exactly as embedding_bag_pooled would.
     With ``use_bins`` the plan owns one workspace, sized for ``max_batch`` samples, whose list
     counter every call leaves at zero (calls on one plan must not overlap).
-
-    ``plan.tile_order(values, offsets)`` computes, on the device, a dispatch order for that batch
-    (each XCD's tiles, most rows first); ``plan(values, offsets, out, tile_order=order)`` then
-    pools the batch in that order, with the same result bit for bit. The order shortens the
-    launch's drain when it is computed off the critical path, e.g. for the next batch on a second
-    stream while the current batch pools; it is ignored by calls with several row shapes.
     """
 
     def __init__(self, tables: Sequence, pooling: str = "sum",
@@ -463,14 +457,13 @@ class PooledEmbedding:
         self._lib = _capi.lib()
         self._fn = self._lib.cti_ebag_forward
         self._ws, self._ws_bytes, self.max_batch = None, 0, int(max_batch)
-        self._probe = None  # stands for the output when an order's row shape is chosen
         if use_bins:
             if self.max_batch <= 0:
                 raise ValueError("use_bins needs max_batch (the largest batch the plan will see)")
             self._ws_bytes = self._lib.cti_ebag_workspace_bytes(self.max_batch, self.num_fields)
             self._ws = torch.zeros(self._ws_bytes, dtype=torch.uint8, device=self.device)
 
-    def _check_batch(self, values: torch.Tensor, offsets: torch.Tensor) -> int:
+    def __call__(self, values: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         if values.device != self.device or offsets.device != self.device:
             raise ValueError(f"values and offsets must be on {self.device}")
         if offsets.dtype != torch.int64 or not offsets.is_contiguous() or not values.is_contiguous():
@@ -478,40 +471,7 @@ class PooledEmbedding:
         n_off = offsets.numel()
         if n_off < 1 or (n_off - 1) % self.num_fields:
             raise ValueError(f"offsets has {n_off} entries; expected F*B+1 with F={self.num_fields}")
-        return (n_off - 1) // self.num_fields
-
-    def tile_order(self, values: torch.Tensor, offsets: torch.Tensor,
-                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Dispatch order for pooling this batch (an int32 device tensor), computed on torch's
-        current stream. ``out`` may be a reused int32 buffer of at least ``order_elements(B)``
-        elements. Raises EbagError (EUNSUPPORTED) for plans whose fields have several row shapes
-        or that hold more than 64 fields."""
-        batch = self._check_batch(values, offsets)
-        n = self.order_elements(batch)
-        if out is None:
-            out = torch.empty(n, dtype=torch.int32, device=self.device)
-        elif out.dtype != torch.int32 or out.numel() < n or not out.is_contiguous() or out.device != self.device:
-            raise ValueError(f"out must be a contiguous int32 tensor of at least {n} elements on {self.device}")
-        stream = torch.cuda.current_stream(self.device).cuda_stream
-        # The output's alignment takes part in choosing the kernel's row shape. The order is made
-        # for an output as torch allocates it (256-byte aligned); a pooling call whose output is
-        # aligned otherwise may run another shape and then ignores the order (detected on the
-        # device).
-        if self._probe is None:
-            self._probe = torch.empty((1, self.width), device=self.device, dtype=self.out_dtype)
-        _capi.check(self._lib.cti_ebag_tile_order(values.data_ptr(), _capi.index_code(values.dtype), values.numel(),
-                                                  offsets.data_ptr(), batch, self.num_fields, self._descs, self._tdt,
-                                                  self._pool, self._probe.data_ptr(), self._odt, self.width,
-                                                  out.data_ptr(), out.numel() * 4, stream))
-        return out
-
-    def order_elements(self, batch: int) -> int:
-        """int32 elements of an order buffer for a batch of ``batch`` samples."""
-        return self._lib.cti_ebag_tile_order_bytes(int(batch), self.num_fields) // 4
-
-    def __call__(self, values: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None,
-                 tile_order: Optional[torch.Tensor] = None) -> torch.Tensor:
-        batch = self._check_batch(values, offsets)
+        batch = (n_off - 1) // self.num_fields
         if out is None:
             out = torch.empty((batch, self.width), device=self.device, dtype=self.out_dtype)
         elif out.dtype != self.out_dtype or tuple(out.shape) != (batch, self.width) or not out.is_contiguous() \
@@ -519,14 +479,6 @@ class PooledEmbedding:
             raise ValueError(f"out must be a contiguous ({batch}, {self.width}) {self.out_dtype} tensor on {self.device}")
         if self._ws is not None and batch > self.max_batch:
             raise ValueError(f"batch {batch} exceeds the plan's max_batch {self.max_batch}")
-        if tile_order is not None:
-            if tile_order.dtype != torch.int32 or not tile_order.is_contiguous() or tile_order.device != self.device:
-                raise ValueError(f"tile_order must be a contiguous int32 tensor on {self.device}")
-            self._opts.tile_order = tile_order.data_ptr()
-            self._opts.tile_order_bytes = tile_order.numel() * 4
-        else:
-            self._opts.tile_order = None
-            self._opts.tile_order_bytes = 0
         stream = torch.cuda.current_stream(self.device).cuda_stream
         _capi.check(self._fn(values.data_ptr(), _capi.index_code(values.dtype), values.numel(), offsets.data_ptr(),
                              batch, self.num_fields, self._descs, self._tdt, self._pool, out.data_ptr(), self._odt,

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define CTI_EBAG_ABI_VERSION 3
+#define CTI_EBAG_ABI_VERSION 2
 
 /* element types of tables and outputs */
 #define CTI_EBAG_F32 0
@@ -91,21 +91,13 @@ typedef struct cti_ebag_table {
  *                    (0 = default, 512).
  *   split_threshold: with use_bins, listed bags up to this length are pooled by one wavefront
  *                    each (lane groups take interleaved rows); longer ones are split across the
- *                    wavefronts of a workgroup (0 = default, 192).
- *   tile_order:      optional device buffer filled by cti_ebag_tile_order for a batch of the
- *                    same shape (same batch size, tables, dtypes, output); the main kernel then
- *                    starts each XCD's tiles with the most rows first. NULL = tile order. Used
- *                    only by jobs of one row shape and at most 64 fields (ignored otherwise); the
- *                    result is the same bit for bit with or without it. An order made for
- *                    another shape is detected on the device and ignored.
- *   tile_order_bytes: size of that buffer (at least cti_ebag_tile_order_bytes(B, F)).         */
+ *                    wavefronts of a workgroup (0 = default, 192).                             */
 typedef struct cti_ebag_options {
   int32_t long_threshold;
   int32_t use_bins;
   int32_t block_threshold;
   int32_t split_threshold;
-  const int32_t* tile_order;
-  int64_t tile_order_bytes;
+  int32_t reserved[4];
 } cti_ebag_options;
 
 /* ABI version this library was built with (CTI_EBAG_ABI_VERSION). */
@@ -162,28 +154,6 @@ int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const 
  * (256 + 24 * batch_size * min(num_fields, 64): list counters, then the field / sample and the
  * value range of each listed bag); -1 for negative arguments. */
 int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fields);
-
-/*
- * Dispatch order for cti_ebag_forward (no counterpart in the reference, whose Triton launch
- * runs one program per bag). A launch ends with a drain: tiles with long bags that start late run
- * on while the rest of the GPU idles. This writes, for the given batch, an order that starts each
- * XCD's tiles with the most rows first (a counting sort of each XCD's tiles by rows per bag, 8
- * workgroups); passing it to cti_ebag_forward (opts->tile_order) for the same batch removes most
- * of the drain (bf16-2m: 36-37 us instead of 40-42). It pays only off the critical path, e.g.
- * computed for the next batch on a second stream while the current one pools, and it can be
- * slower on cold, DRAM-bound batches (lazy-32k: 302 us instead of 274), so it is opt-in.
- * Arguments as for cti_ebag_forward (values are not read); `order` is a device buffer of
- * `order_bytes` >= cti_ebag_tile_order_bytes(batch_size, num_fields). Returns
- * CTI_EBAG_EUNSUPPORTED for jobs of several row shapes or more than 64 fields.
- */
-int cti_ebag_tile_order(const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
-                        int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables,
-                        int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
-                        int64_t out_row_stride, int32_t* order, int64_t order_bytes, void* stream);
-
-/* Bytes of an order buffer for any job of batch_size samples and num_fields fields
- * (16 + 4 * batch_size * min(num_fields, 64)); -1 for negative arguments. */
-int64_t cti_ebag_tile_order_bytes(int64_t batch_size, int32_t num_fields);
 
 /*
  * Device packer for the reference flat layout (online_best/infer.py:960-974, and the

@@ -23,7 +23,7 @@ def test_header_declares_the_entry_points():
               "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version", "cti_ebag_layernorm",
               "cti_ebag_fused_all_slots_int8", "cti_ebag_quantize_int8", "cti_ebag_fused_all_slots_typed",
               "cti_ebag_narrow_ids", "cti_ebag_stage_copy", "cti_ebag_stage_offset",
-              "cti_ebag_fused_all_slots_layernorm", "cti_ebag_tile_order", "cti_ebag_tile_order_bytes"):
+              "cti_ebag_fused_all_slots_layernorm"):
         assert n in names
 
 
@@ -343,64 +343,3 @@ def test_narrow_ids_in_a_forked_child(pkg):
             os._exit(code)
     _, status = os.waitpid(pid, 0)
     assert os.WIFEXITED(status) and os.WEXITSTATUS(status) == 0
-
-
-def test_options_struct_matches_header(pkg):
-    """Field order and size of cti_ebag_options as the header declares it."""
-    text = open(HEADER).read()
-    body = re.search(r"typedef struct cti_ebag_options \{(.*?)\} cti_ebag_options;", text, re.S).group(1)
-    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
-    fields = re.findall(r"(\w+)\s*;", body)
-    assert fields == [f[0] for f in pkg._capi.Options._fields_]
-    assert ctypes.sizeof(pkg._capi.Options) == 32
-
-
-def test_tile_order_bytes(pkg):
-    lib = pkg._capi.lib()
-    assert lib.cti_ebag_tile_order_bytes(4096, 28) == 16 + 4 * 4096 * 28
-    assert lib.cti_ebag_tile_order_bytes(10, 100) == 16 + 4 * 10 * 64
-    assert lib.cti_ebag_tile_order_bytes(-1, 3) < 0
-
-
-# Every call below fails a host check before any HIP call: none may reach a launch, since the
-# pointers are placeholders.
-def _order(pkg, order=64, order_bytes=8, **kw):
-    c = pkg._capi
-    args = dict(values=1, index_type=c.I64, nnz=10, offsets=1, batch=4, num_fields=1, tables=_table(pkg), tdt=c.BF16,
-                pooling=c.SUM, out=256, odt=c.BF16, stride=128)
-    args.update(kw)
-    return c.lib().cti_ebag_tile_order(args["values"], args["index_type"], args["nnz"], args["offsets"],
-                                       args["batch"], args["num_fields"], args["tables"], args["tdt"], args["pooling"],
-                                       args["out"], args["odt"], args["stride"], order, order_bytes, None)
-
-
-def test_tile_order_rejects_bad_arguments(pkg):
-    c = pkg._capi
-    assert _order(pkg, order=None) == c.EINVAL and "order buffer is NULL" in c.last_error()
-    assert _order(pkg, order=66) == c.EINVAL and "aligned" in c.last_error()
-    assert _order(pkg, tdt=9) == c.EINVAL and "table dtype" in c.last_error()
-    # 4 samples of one 256-byte-row field are one tile: 4 header words + 1 entry = 20 bytes
-    assert _order(pkg, order_bytes=16) == c.EINVAL and "order buffer of 16 bytes" in c.last_error()
-
-
-def test_tile_order_needs_one_row_shape(pkg):
-    c = pkg._capi
-    t = (c.Table * 2)()
-    for i, (dim, col) in enumerate(((128, 0), (32, 128))):  # 256-byte and 64-byte bf16 rows
-        t[i].data, t[i].rows, t[i].row_stride, t[i].dim, t[i].out_col, t[i].row_scale = 64, 100, dim, dim, col, None
-    assert _order(pkg, num_fields=2, tables=t, stride=160, order_bytes=1 << 20) == c.EUNSUPPORTED
-    assert "one row shape" in c.last_error()
-
-
-def test_forward_rejects_a_short_or_misaligned_tile_order(pkg):
-    c = pkg._capi
-    o = c.Options()
-    # an aligned output selects the 16-lane pooling kernel, which takes orders: one tile here,
-    # so 16 bytes are too few (an unaligned output would select the element-wise kernel, which
-    # ignores orders and would launch)
-    o.tile_order, o.tile_order_bytes = 64, 16
-    assert _forward(pkg, tables=_table(pkg), out=256, opts=ctypes.byref(o)) == c.EINVAL
-    assert "tile order of 16 bytes" in c.last_error()
-    o.tile_order, o.tile_order_bytes = 66, 1 << 20
-    assert _forward(pkg, tables=_table(pkg), out=256, opts=ctypes.byref(o)) == c.EINVAL
-    assert "aligned" in c.last_error()
