@@ -408,7 +408,8 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int fi, int local
   int rank = 0;
   // unrolled by at most 8: each unrolled readlane holds a scalar register, and 32 or 64 of them
   // (tiles of narrow rows) would cap the wavefronts per SIMD by scalar registers
-#pragma unroll(NB < 8 ? NB : 8)
+  constexpr int kRankUnroll = NB < 8 ? NB : 8;
+#pragma unroll kRankUnroll
   for (int j = 0; j < NB; ++j) {
     const int kj = __builtin_amdgcn_readlane(key, j);
     rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
