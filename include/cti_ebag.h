@@ -61,7 +61,7 @@ extern "C" {
 /* status codes */
 #define CTI_EBAG_OK 0
 #define CTI_EBAG_EINVAL (-1)      /* bad argument (null pointer, negative size, bad enum, ...) */
-#define CTI_EBAG_EUNSUPPORTED (-2) /* well-formed but outside what this build implements */
+#define CTI_EBAG_EUNSUPPORTED (-2) /* well-formed but outside what the library implements */
 #define CTI_EBAG_EHIP (-3)        /* a HIP runtime call failed (message carries hipGetErrorString) */
 #define CTI_EBAG_EWORKSPACE (-4)  /* workspace missing or smaller than cti_ebag_workspace_bytes() */
 

@@ -1,7 +1,7 @@
 /*
  * ORACLE — test infrastructure, not product code.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this library,
- * and only as the checker (or the timed CPU baseline); the product path never calls it.
+ * and only to check results against (or as the timed CPU baseline); the product path never calls it.
  *
  * CPU restatement of the fused multi-field embedding-bag step:
  *   - online_best/infer.py:805-827  fused_all_slots_embedding_kernel: per (sample b, slot s),

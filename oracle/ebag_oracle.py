@@ -1,7 +1,7 @@
 """ORACLE — test infrastructure, not product code.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module,
-and only as the checker (or the timed CPU baseline). The product path never calls it.
+and only to check results against (or as the timed CPU baseline). The product path never calls it.
 
 CPU restatements of the fused sparse-feature embedding-bag path:
   pool / pool_c      the pooling step, in C (ebag_oracle.c, OpenMP over samples)
