@@ -235,6 +235,27 @@ def test_edge_shapes(pkg, dev):
         assert np.array_equal(got, want), kw
 
 
+@pytest.mark.parametrize("path", [dict(), dict(use_bins=True), dict(use_bins=True, split_threshold=100000000),
+                                  dict(long_threshold=-1)])
+def test_one_bag_of_five_million_rows(pkg, dev, path):
+    # the longest bags the layout allows: 5,000,000 rows in one bag beside an empty and a short
+    # one, pooled by one wavefront (no binning, or binned below the split length), by the 8
+    # wavefronts of a list workgroup (binned and split), or with every bag split. Rows in
+    # {-1, 0, 1}: every fp32 partial sum stays below 2^24 and is exact, so all paths equal the
+    # int64 sums bit for bit.
+    rng = np.random.default_rng(77)
+    V, D, lens = 3000, 64, np.array([0, 5_000_000, 7])
+    rows = rng.integers(-1, 2, (V, D)).astype(np.float32)
+    ids = rng.integers(-5, V + 5, int(lens.sum()))
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    want = np.zeros((3, D), np.int64)
+    clamped = np.clip(ids, 0, V - 1)
+    for b in range(3):  # row counts times rows: the int64 sum of the bag's rows
+        want[b] = np.bincount(clamped[offsets[b]:offsets[b + 1]], minlength=V) @ rows.astype(np.int64)
+    got = gpu_pool(pkg, dev, ids, offsets, [orc.encode(rows, "bf16")], "bf16", "sum", "f32", **path)
+    assert np.array_equal(got, want.astype(np.float32))
+
+
 # ---- reference layout (drop-in entry point) and the RepEncoder caller --------------------------
 def _reference_batch(seed, S=28, B=64, V=5000, D=128, dt="bf16", max_len=12):
     case = random_case(seed, F=S, B=B, dims=(D,), V=(V,), tdt=dt, max_len=max_len)
