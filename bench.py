@@ -63,21 +63,27 @@ WORKLOAD_TEXT = {
     "lazy-32k": "28 fields, bf16 tables 4,000,000 x 128, B=32768 from 8 merged sub-batches, Zipf(0.8), mean",
     "small-fp32": "28 fields, fp32 tables 10,000 x 64, B=256, Poisson(3) lengths, sum",
 }
+# Workloads whose launches end faster when tiles start longest-first (the order is made one step
+# ahead inside the previous launch). lazy-32k is slower with it (its launch is DRAM-bound and the
+# reordered tiles read values out of address order), small-fp32 too (launch-bound), int8 unchanged.
+ORDERED_BY_DEFAULT = {"bf16-2m", "fp32-1m"}
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def traffic_from_profiles(workload, kernel="pool_kernel"):
-    """HBM bytes per launch recorded by the rocprofv3 counter runs, read from the line
-    `hbm_bytes_per_launch: N` of profiles/<kernel>_<workload>.md, or None."""
+def traffic_from_profiles(workload, kernel="pool_kernel", keys=("hbm_bytes_per_launch",)):
+    """HBM bytes per launch recorded by the rocprofv3 counter runs, read from the first of the
+    lines `<key>: N` (in the order of `keys`) of profiles/<kernel>_<workload>.md, or None."""
     path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}.md")
     if not os.path.exists(path):
         return None
     with open(path) as fh:
-        for line in fh:
-            if line.strip().startswith("hbm_bytes_per_launch:"):
+        lines = [line.strip() for line in fh]
+    for key in keys:
+        for line in lines:
+            if line.startswith(key + ":"):
                 return float(line.split(":", 1)[1].strip())
     return None
 
@@ -509,7 +515,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # 300 untimed steps (~12 ms): the first ~10 ms of sustained load run 1-3 us per step slower
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="bf16-2m", choices=sorted(WORKLOAD_TEXT))
     ap.add_argument("--sets", type=int, default=8, help="independently seeded index sets rotated over")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -522,9 +529,16 @@ def main():
                     help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
                          "step end to end from host batches")
     ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
+    ap.add_argument("--dispatch-order", choices=["auto", "on", "off"], default="auto",
+                    help="on: each step also sorts the next batch's tiles (most rows per bag first) and follows "
+                         "the order the previous step made; auto: on for the workloads where that was measured "
+                         "to pay (%s) without --bins" % ", ".join(sorted(ORDERED_BY_DEFAULT)))
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times (scales rocprofv3 FETCH/WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.dispatch_order == "auto":
+        args.dispatch_order = "on" if args.workload in ORDERED_BY_DEFAULT and not args.bins else "off"
+    args.dispatch_order = args.dispatch_order == "on"
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -572,7 +586,7 @@ def main():
     plan = pkg.PooledEmbedding(pooled_tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype,
                                long_threshold=args.long_threshold, use_bins=args.bins,
                                block_threshold=args.block_threshold, max_batch=wl0.batch,
-                               split_threshold=args.split_threshold)
+                               split_threshold=args.split_threshold, dispatch_order=args.dispatch_order)
     out = torch.empty((wl0.batch, sum(wl0.dims)), dtype=wl0.out_dtype, device=dev)
     if args.stage == "layernorm":
         return bench_layernorm(args, pkg, plan, inputs, wl0, dev)
@@ -580,10 +594,16 @@ def main():
     bytes_comp = [wl.bytes_compulsory(int8=args.int8) for wl in wls]
     torch.cuda.synchronize()
 
+    def step(i):
+        v, o = inputs[i % args.sets]
+        if args.dispatch_order:
+            plan(v, o, out, next_offsets=inputs[(i + 1) % args.sets][1])
+        else:
+            plan(v, o, out)
+
     log(f"warmup {args.warmup} steps")
     for i in range(args.warmup):
-        v, o = inputs[i % args.sets]
-        plan(v, o, out)
+        step(i)
     torch.cuda.synchronize()
 
     # Timed region: K back-to-back steps, bracketed by one pair of HIP events recorded on the
@@ -595,15 +615,15 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record()
-    for i in range(K):
-        v, o = inputs[i % args.sets]
-        plan(v, o, out)
+    for i in range(args.warmup, args.warmup + K):  # continues the warm-up's sequence of index sets
+        step(i)
     ev1.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     mean_launch_s = ev0.elapsed_time(ev1) / 1e3 / K
-    used_bytes = float(np.mean([bytes_alg[i % args.sets] for i in range(K)]))
-    used_comp = float(np.mean([bytes_comp[i % args.sets] for i in range(K)]))
+    timed = range(args.warmup, args.warmup + K)
+    used_bytes = float(np.mean([bytes_alg[i % args.sets] for i in timed]))
+    used_comp = float(np.mean([bytes_comp[i % args.sets] for i in timed]))
     ms_per_step = elapsed / K * 1e3
     value = wl0.num_bags / (elapsed / K)
     achieved = used_bytes / mean_launch_s / 1e9
@@ -652,10 +672,14 @@ def main():
         "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}", "batch": wl0.batch,
                    "fields": wl0.num_fields, "dims": sorted(set(wl0.dims)), "pooling": wl0.pooling,
                    "nnz_mean": float(np.mean([wl.nnz for wl in wls])), "index_sets": args.sets,
-                   "length_binning": bool(args.bins), "int8_tables": bool(args.int8)},
+                   "length_binning": bool(args.bins), "int8_tables": bool(args.int8),
+                   "dispatch_order": bool(args.dispatch_order)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic_from_profiles(args.workload + ("-int8" if args.int8 else ""), prof_kernel),
+                     "traffic": traffic_from_profiles(
+                         args.workload + ("-int8" if args.int8 else ""), prof_kernel,
+                         ("hbm_bytes_per_launch",) if args.dispatch_order
+                         else ("hbm_bytes_per_launch_order_off", "hbm_bytes_per_launch")),
                      "kernel": kernel_name,
                      "bytes_per_launch": used_bytes,
                      "compulsory_bytes_per_launch": used_comp, "launch_us_mean": mean_launch_s * 1e6},

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must precede the dlopen below, see module docstring
 LIB_NAME = "libcti_ebag.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, BF16, F16, I8 = 0, 1, 2, 3
 I64, I32 = 0, 1
@@ -61,7 +61,10 @@ class Options(ctypes.Structure):
         ("use_bins", ctypes.c_int32),
         ("block_threshold", ctypes.c_int32),
         ("split_threshold", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 4),
+        ("tile_order", ctypes.c_void_p),
+        ("next_order", ctypes.c_void_p),
+        ("next_offsets", ctypes.c_void_p),
+        ("order_bytes", ctypes.c_int64),
     ]
 
 
@@ -85,6 +88,7 @@ SIGNATURES = {
          ctypes.POINTER(Options), _P],
     ),
     "cti_ebag_workspace_bytes": (ctypes.c_int64, [_I64, _I32]),
+    "cti_ebag_order_bytes": (ctypes.c_int64, [_I64, _I32]),
     "cti_ebag_pack_slots": (ctypes.c_int, [_PP, _PP, _PI64, _I32, _I64, _P, _P, _P, _P, _P]),
     "cti_ebag_merge_batches": (
         ctypes.c_int,

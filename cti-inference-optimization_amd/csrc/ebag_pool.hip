@@ -28,6 +28,10 @@
 //     completes under the current chunk's row loads. Tables under 4 GiB with power-of-two row sizes are read with buffer
 //     loads: a row's offset is one shift-add, and rows past a bag's end use an out-of-range offset
 //     that returns zeros without a memory request (no per-row branch).
+//   * Dispatch order (optional): a launch can follow a tile order made one batch ahead, in which
+//     each XCD starts its tiles with the most rows per bag, and make the next batch's order in a
+//     few extra workgroups at its first dispatch positions. It shortens the launch's drain; the
+//     results do not depend on it.
 //   * Mean: one fp64 reciprocal per bag, RN32(RN64(sum * 1/L)) per element, which equals the IEEE
 //     fp32 division except for quotients below the normal range (those take the division).
 //     Conversions to bf16 use the hardware round-to-nearest-even pack.
@@ -146,6 +150,10 @@ struct PoolParams {
   int64_t split_threshold;  // listed bags longer than this are split over a workgroup
   unsigned int* bin_count;  // binning: list lengths being built (NULL without binning): [0] one-wave, [2] split
   unsigned int* bin_total;  // binning: list lengths handed to the list kernel: [0] one-wave, [2] split
+  const int32_t* tile_order;  // optional dispatch order of this launch (layout at kOrderMagic), NULL = none
+  int32_t* next_order;        // optional: the first kOrderBlocks workgroups write the next batch's order here
+  const void* next_offsets;   // the next batch's bag offsets (type and layout of `offsets`)
+  int32_t order_blocks;       // with next_order: workgroups that make it (8 x chunks per XCD range)
   int32_t num_fields;
   int32_t num_tiles;
   int32_t tiles_per_field;  // every field of a launch has the same number of tiles
@@ -181,12 +189,17 @@ __device__ __forceinline__ int xcd_contiguous(int bid, int n) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + s;
 }
 
-__device__ __forceinline__ int block_tile() {
+// Tile position of dispatch position `pos` in a launch of n tiles.
+__device__ __forceinline__ int xcd_position(int pos, int n) {
 #if CTI_EBAG_XCD_REMAP
-  return xcd_contiguous(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  return xcd_contiguous(pos, n);
 #else
-  return static_cast<int>(blockIdx.x);
+  return pos;
 #endif
+}
+
+__device__ __forceinline__ int block_tile() {
+  return xcd_position(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
 }
 
 // Buffer resource over one table: 32-bit byte offsets, offsets at or past the span read as zeros.
@@ -499,14 +512,141 @@ __device__ __forceinline__ void bin_handoff(const PoolParams& p) {
   }
 }
 
-// Main kernel: one wavefront per workgroup, one tile per workgroup.
+// ---------------------------------------------------------------------------------------------
+// Dispatch order. Workgroups are dealt to the XCDs round-robin and xcd_contiguous() gives XCD x
+// a contiguous range of tile positions, which it starts in order as wavefront slots free up. A
+// launch ends with a drain: tiles of long bags that start late run on while the rest of the chip
+// idles. Starting each XCD's tiles with the most rows per bag first removes most of that drain.
+// The order of a batch is made one launch ahead: a launch given `next_order` runs order_blocks
+// extra workgroups at the first dispatch positions (a multiple of 8, so every tile keeps its
+// XCD), each sorting one chunk of kOrderChunk tiles of one XCD range of the next batch by rows per
+// bag while the rest of the launch pools; the next launch on the stream reads it as `tile_order`. Only the sequence of each XCD's
+// tiles changes and each output row keeps one writer, so results do not depend on the order.
+//
+// Order buffer (int32): [0] tiles of the launch it was made for, [1] kOrderMagic, [2..3] zero,
+// [kOrderHeader + position] = tile. A launch follows an order only if [0] and [1] match it, and
+// takes its own position for any entry outside its tiles, so no buffer can make it read or write
+// out of bounds; an order written here for any launch of as many tiles is a permutation of them.
+constexpr int32_t kOrderMagic = 0x4f524452;
+constexpr int kOrderHeader = 4;
+constexpr int kOrderChunk = 2048;   // an XCD range is sorted in chunks of this many tiles
+constexpr int kOrderBuckets = 64;   // rows per bag 63, 62, ..., 0 (more count as 63)
+constexpr int kOrderUnroll = 8;     // tiles per lane whose offsets are loaded together
+static_assert(kOrderBuckets == kWave, "one bucket per lane in the prefix sum");
+
+struct OrderLds {
+  unsigned char bucket[kOrderChunk];
+  unsigned int next[kOrderBuckets];
+};
+
+__device__ __forceinline__ int ordered_tile(const PoolParams& p, int pos) {
+  if (!p.tile_order) return pos;
+  // the host checked that the buffer holds kOrderHeader + num_tiles entries
+  const int32_t n = p.tile_order[0], magic = p.tile_order[1], t = p.tile_order[kOrderHeader + pos];
+  return n == p.num_tiles && magic == kOrderMagic && t >= 0 && t < p.num_tiles ? t : pos;
+}
+
+// Rows of tile t (NB consecutive bags of one field) in the next batch, from its offsets alone. A
+// launch that makes an order holds every field of its job in job order (the host checks it), so
+// field fi's offsets start at fi * offsets_stride: no dependent load of the field's index, which
+// would make each tile's offset loads wait for the previous tile's (loads complete in order).
+__device__ __forceinline__ int64_t next_tile_rows(const PoolParams& p, int t, int nb) {
+  const int fi = t / p.tiles_per_field;
+  const int64_t b0 = static_cast<int64_t>(t - fi * p.tiles_per_field) * nb;
+  const int64_t b1 = b0 + nb < p.batch ? b0 + nb : p.batch;
+  const int64_t i = static_cast<int64_t>(fi) * p.offsets_stride;
+  return load_offset(p, p.next_offsets, i + b1) - load_offset(p, p.next_offsets, i + b0);  // val_base cancels
+}
+
+// One wavefront sorts chunk `chunk` of XCD range x of the next batch's tiles, most rows per bag
+// first: a counting sort whose bucket of each tile is computed once and kept in LDS, so the
+// positions it hands out are a permutation of the chunk whatever the offsets hold (the order
+// inside a bucket is whatever the LDS atomics give).
+template <int NB>
+__device__ void order_next(const PoolParams& p, int x, int chunk, OrderLds& s) {
+  const int n = p.num_tiles;
+  const int q = n >> 3, r = n & 7;
+  const int lo = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+  const int cnt = q + (x < r ? 1 : 0);
+  const int lane = lane_id();
+  int32_t* const order = p.next_order + kOrderHeader;
+  const int c0 = chunk * kOrderChunk;
+  if (c0 < cnt) {
+    const int m = cnt - c0 < kOrderChunk ? cnt - c0 : kOrderChunk;
+    s.next[lane] = 0u;
+    __syncthreads();
+    for (int k0 = 0; k0 < m; k0 += kOrderUnroll * kWave) {
+      int64_t rows[kOrderUnroll];
+#pragma unroll
+      for (int u = 0; u < kOrderUnroll; ++u) {
+        const int k = k0 + u * kWave + lane;
+        rows[u] = k < m ? next_tile_rows(p, lo + c0 + k, NB) : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kOrderUnroll; ++u) {
+        const int k = k0 + u * kWave + lane;
+        if (k < m) {
+          int64_t per_bag = rows[u] / NB;
+          per_bag = per_bag < 0 ? 0 : (per_bag > kOrderBuckets - 1 ? kOrderBuckets - 1 : per_bag);
+          const int b = kOrderBuckets - 1 - static_cast<int>(per_bag);
+          s.bucket[k] = static_cast<unsigned char>(b);
+          atomicAdd(&s.next[b], 1u);
+        }
+      }
+    }
+    __syncthreads();
+    // exclusive prefix sum of the bucket counts, bucket = lane
+    const unsigned int c = s.next[lane];
+    unsigned int incl = c;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const unsigned int v = __shfl_up(incl, d);
+      if (lane >= d) incl += v;
+    }
+    s.next[lane] = incl - c;
+    __syncthreads();
+    for (int k0 = 0; k0 < m; k0 += kOrderUnroll * kWave) {
+      unsigned int at[kOrderUnroll];
+#pragma unroll
+      for (int u = 0; u < kOrderUnroll; ++u) {
+        const int k = k0 + u * kWave + lane;
+        at[u] = k < m ? atomicAdd(&s.next[s.bucket[k]], 1u) : 0u;  // in [0, m)
+      }
+#pragma unroll
+      for (int u = 0; u < kOrderUnroll; ++u) {
+        const int k = k0 + u * kWave + lane;
+        if (k < m) order[lo + c0 + static_cast<int>(at[u])] = lo + c0 + k;
+      }
+    }
+  }
+  if (x == 0 && chunk == 0 && lane == 0) {
+    p.next_order[0] = n;
+    p.next_order[1] = kOrderMagic;
+    p.next_order[2] = 0;
+    p.next_order[3] = 0;
+  }
+}
+
+// Main kernel: one wavefront per workgroup, one tile per workgroup (after the order workgroups,
+// when the launch makes the next batch's order).
 template <typename TT, typename OT, int LANES, int VPL, bool BUF>
 __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
-  __shared__ TileLdsOf<TT, LANES, VPL> s;
+  __shared__ union {
+    TileLdsOf<TT, LANES, VPL> tile;
+    OrderLds order;
+  } s;
   bin_handoff(p);
-  const int tile = block_tile();
+  int pos = static_cast<int>(blockIdx.x);
+  if (p.next_order) {
+    if (pos < p.order_blocks) {
+      order_next<TileShape<TT, LANES, VPL>::NB>(p, pos & 7, pos >> 3, s.order);
+      return;
+    }
+    pos -= p.order_blocks;
+  }
+  const int tile = ordered_tile(p, xcd_position(pos, p.num_tiles));
   const int fi = tile / p.tiles_per_field;
-  pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s);
+  pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s.tile);
 }
 
 // Main kernel of a mixed-width launch: the fields' rows differ in width but each is one lane
@@ -1148,7 +1288,8 @@ unsigned list_blocks(const PoolParams& p) {
 template <typename TT, typename OT, int LANES, int VPL>
 void launch_shape(const PoolParams& p, const LongList* l, hipStream_t s) {
   if (l) launch_bins(p, *l, s);
-  const dim3 grid(static_cast<unsigned>(p.num_tiles)), block(kMainThreads);
+  const dim3 grid(static_cast<unsigned>(p.num_tiles) + (p.next_order ? static_cast<unsigned>(p.order_blocks) : 0u)),
+      block(kMainThreads);
   if (p.buffer_ok)
     hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true>), grid, block, 0, s, p);
   else
@@ -1234,6 +1375,10 @@ struct Job {
   int32_t block_threshold;  // 0 = default (with bins)
   int32_t split_threshold;  // 0 = default (with bins)
   void* workspace;
+  const int32_t* tile_order;  // optional dispatch order (kOrderMagic layout)
+  int32_t* next_order;        // optional: make the next batch's order here
+  const void* next_offsets;
+  int64_t order_bytes;        // size of each order buffer
 };
 
 int validate_tables(const Job& j) {
@@ -1285,6 +1430,23 @@ int run_job(const Job& j, hipStream_t stream) {
     }
   }
   const bool mixed = one_vec_shapes > 1;
+  // A dispatch order belongs to a job that is one main-kernel launch of one fixed row shape.
+  const bool ordered = j.tile_order || j.next_order;
+  if (ordered) {
+    bool one_shape = j.num_fields <= kMaxFields && !j.use_bins && var[0] != kVarGeneric;
+    for (int f = 1; f < j.num_fields; ++f) one_shape = one_shape && var[f] == var[0];
+    if (!one_shape)
+      return set_error(CTI_EBAG_EUNSUPPORTED,
+                       "a dispatch order needs one row shape with aligned rows, at most %d fields and no binning",
+                       kMaxFields);
+    const int bpt = bags_per_tile(var[0]);
+    const int64_t tiles = static_cast<int64_t>(j.num_fields) * ((j.batch + bpt - 1) / bpt);
+    if (tiles > INT32_MAX / 2)
+      return set_error(CTI_EBAG_EUNSUPPORTED, "batch of %lld samples has too many tiles to order", (long long)j.batch);
+    if (j.order_bytes < (kOrderHeader + tiles) * 4)
+      return set_error(CTI_EBAG_EINVAL, "order buffers of %lld bytes; this job needs %lld", (long long)j.order_bytes,
+                       (long long)((kOrderHeader + tiles) * 4));
+  }
   for (int v = 0; v <= kVarMixed; ++v) {
     std::vector<int> fields;
     if (v == kVarMixed) {
@@ -1322,6 +1484,13 @@ int run_job(const Job& j, hipStream_t stream) {
       if (v != kVarGeneric && p.sub_threshold > kMaxShortBag) p.sub_threshold = kMaxShortBag;
       p.bin_count = bins ? list.count : nullptr;
       p.bin_total = bins ? list.total : nullptr;
+      if (ordered) {  // the job's only launch: fields 0 .. F-1 in job order
+        if (c0 != 0 || fields.size() != static_cast<size_t>(j.num_fields))
+          return set_error(CTI_EBAG_EUNSUPPORTED, "internal: an ordered job must be one launch");
+        p.tile_order = j.tile_order;
+        p.next_order = j.next_order;
+        p.next_offsets = j.next_offsets;
+      }
       const size_t nf = fields.size() - c0 < static_cast<size_t>(kMaxFields) ? fields.size() - c0 : kMaxFields;
       p.num_fields = static_cast<int32_t>(nf);
       bool all_buf = true;
@@ -1355,6 +1524,10 @@ int run_job(const Job& j, hipStream_t stream) {
       p.num_tiles = static_cast<int32_t>(tiles);
       // every field of a single-shape launch has the same number of tiles
       p.tiles_per_field = static_cast<int32_t>(tiles / static_cast<int64_t>(nf));
+      if (p.next_order) {  // one workgroup per chunk of each XCD range
+        const int64_t per_range = (tiles + 7) / 8;
+        p.order_blocks = static_cast<int32_t>(8 * ((per_range + kOrderChunk - 1) / kOrderChunk));
+      }
       const hipError_t e = launch_typed(j.tdt, j.odt, v, p, bins ? &list : nullptr, stream);
       if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "pooling kernel launch failed: %s", hipGetErrorString(e));
     }
@@ -1608,6 +1781,12 @@ extern "C" int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fiel
   return workspace_bytes(batch_size, num_fields);
 }
 
+extern "C" int64_t cti_ebag_order_bytes(int64_t batch_size, int32_t num_fields) {
+  if (batch_size < 0 || num_fields < 0) return -1;
+  const int64_t per_launch = num_fields < kMaxFields ? num_fields : kMaxFields;
+  return (kOrderHeader + batch_size * per_launch) * 4;  // at least one bag per tile
+}
+
 extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
                                 int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables,
                                 int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
@@ -1650,6 +1829,21 @@ extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t 
     j.use_bins = opts->use_bins != 0;
     j.block_threshold = opts->block_threshold;
     j.split_threshold = opts->split_threshold;
+    j.tile_order = opts->tile_order;
+    j.next_order = opts->next_order;
+    j.next_offsets = opts->next_offsets;
+    j.order_bytes = opts->order_bytes;
+  }
+  if (j.tile_order || j.next_order) {
+    if (reinterpret_cast<uintptr_t>(j.tile_order) % 4 != 0 || reinterpret_cast<uintptr_t>(j.next_order) % 4 != 0)
+      return set_error(CTI_EBAG_EINVAL, "order buffers must be 4-byte aligned");
+    if (j.next_order && !j.next_offsets) return set_error(CTI_EBAG_EINVAL, "next_order given without next_offsets");
+    if (j.order_bytes <= 0) return set_error(CTI_EBAG_EINVAL, "order_bytes must be > 0 (got %lld)", (long long)j.order_bytes);
+    if (j.tile_order && j.next_order) {
+      const uintptr_t a = reinterpret_cast<uintptr_t>(j.tile_order), b = reinterpret_cast<uintptr_t>(j.next_order);
+      if (a < b + static_cast<uintptr_t>(j.order_bytes) && b < a + static_cast<uintptr_t>(j.order_bytes))
+        return set_error(CTI_EBAG_EINVAL, "tile_order and next_order overlap (the launch reads one and writes the other)");
+    }
   }
   if (j.use_bins) {
     const int64_t need = workspace_bytes(batch_size, num_fields);

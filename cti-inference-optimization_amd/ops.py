@@ -436,12 +436,19 @@ class PooledEmbedding:
     ``plan(values, offsets, out=None)`` pools one batch exactly as embedding_bag_pooled would.
     With ``use_bins`` the plan owns one workspace, sized for ``max_batch`` samples, whose list
     counter every call leaves at zero (calls on one plan must not overlap).
+
+    With ``dispatch_order`` a serving loop passes the next batch's offsets with each call
+    (``plan(values, offsets, out, next_offsets=...)``): the launch also sorts that batch's tiles,
+    most rows per bag first within each XCD's share, and the next call follows that order, which
+    shortens the drain at the end of its launch. The plan alternates two device order buffers;
+    the output is the same bit for bit with or without an order, whatever batch comes next. Only
+    for jobs of one tiled row shape without binning (the library raises otherwise).
     """
 
     def __init__(self, tables: Sequence, pooling: str = "sum",
                  out_dtype: Optional[torch.dtype] = None, long_threshold: int = 0,
                  use_bins: bool = False, block_threshold: int = 0, max_batch: int = 0,
-                 split_threshold: int = 0):
+                 split_threshold: int = 0, dispatch_order: bool = False):
         self.tables = list(tables)  # keeps the tensors (and int8 scales) alive
         self._descs, self.device, self._tdt, self.width, tdt = _table_descs(self.tables)
         self.num_fields = len(self.tables)
@@ -462,8 +469,22 @@ class PooledEmbedding:
                 raise ValueError("use_bins needs max_batch (the largest batch the plan will see)")
             self._ws_bytes = self._lib.cti_ebag_workspace_bytes(self.max_batch, self.num_fields)
             self._ws = torch.zeros(self._ws_bytes, dtype=torch.uint8, device=self.device)
+        if dispatch_order and use_bins:
+            raise ValueError("dispatch_order does not combine with use_bins")
+        self.dispatch_order = bool(dispatch_order)
+        self._orders, self._order_bytes = None, 0
+        self._cur, self._have_order = 0, False  # _orders[_cur] holds the order of the coming batch
 
-    def __call__(self, values: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def _order_buffers(self, batch: int):
+        need = self._lib.cti_ebag_order_bytes(max(batch, self.max_batch), self.num_fields)
+        if need > self._order_bytes:
+            n = (need + 3) // 4
+            self._orders = [torch.zeros(n, dtype=torch.int32, device=self.device) for _ in range(2)]
+            self._order_bytes, self._cur, self._have_order = 4 * n, 0, False
+        return self._orders
+
+    def __call__(self, values: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None,
+                 next_offsets: Optional[torch.Tensor] = None) -> torch.Tensor:
         if values.device != self.device or offsets.device != self.device:
             raise ValueError(f"values and offsets must be on {self.device}")
         if offsets.dtype != torch.int64 or not offsets.is_contiguous() or not values.is_contiguous():
@@ -479,11 +500,29 @@ class PooledEmbedding:
             raise ValueError(f"out must be a contiguous ({batch}, {self.width}) {self.out_dtype} tensor on {self.device}")
         if self._ws is not None and batch > self.max_batch:
             raise ValueError(f"batch {batch} exceeds the plan's max_batch {self.max_batch}")
+        if next_offsets is not None:
+            if not self.dispatch_order:
+                raise ValueError("next_offsets needs a plan made with dispatch_order=True")
+            if next_offsets.device != self.device or next_offsets.dtype != torch.int64 \
+                    or not next_offsets.is_contiguous() or next_offsets.numel() != n_off:
+                raise ValueError(f"next_offsets must be contiguous int64 with {n_off} entries on {self.device}")
         stream = torch.cuda.current_stream(self.device).cuda_stream
+        opts = self._opts  # read by the C call before it returns
+        if self.dispatch_order:
+            orders = self._order_buffers(batch)
+            opts.tile_order = orders[self._cur].data_ptr() if self._have_order else None
+            opts.next_order = orders[1 - self._cur].data_ptr() if next_offsets is not None else None
+            opts.next_offsets = next_offsets.data_ptr() if next_offsets is not None else None
+            opts.order_bytes = self._order_bytes
         _capi.check(self._fn(values.data_ptr(), _capi.index_code(values.dtype), values.numel(), offsets.data_ptr(),
                              batch, self.num_fields, self._descs, self._tdt, self._pool, out.data_ptr(), self._odt,
                              self.width, self._ws.data_ptr() if self._ws is not None else None, self._ws_bytes,
-                             self._opts, stream))
+                             opts, stream))
+        if self.dispatch_order:
+            if next_offsets is not None:
+                self._cur, self._have_order = 1 - self._cur, True
+            else:
+                self._have_order = False
         return out
 
 

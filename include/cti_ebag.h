@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define CTI_EBAG_ABI_VERSION 2
+#define CTI_EBAG_ABI_VERSION 3
 
 /* element types of tables and outputs */
 #define CTI_EBAG_F32 0
@@ -91,13 +91,32 @@ typedef struct cti_ebag_table {
  *                    (0 = default, 512).
  *   split_threshold: with use_bins, listed bags up to this length are pooled by one wavefront
  *                    each (lane groups take interleaved rows); longer ones are split across the
- *                    wavefronts of a workgroup (0 = default, 192).                             */
+ *                    wavefronts of a workgroup (0 = default, 192).
+ * Dispatch order (no counterpart in the reference, whose Triton launch runs one program per bag).
+ * A launch ends with a drain: tiles of long bags that start late run on while the rest of the GPU
+ * idles. A serving loop that knows its next batch lets each call sort that batch's tiles, most
+ * rows per bag first within each XCD's share, in 8 extra workgroups of the current launch; the
+ * next call follows that order. Results are the same bit for bit with or without an order.
+ *   tile_order:      device buffer written by an earlier call's next_order (NULL = none). An
+ *                    order made for a launch of another tile count is detected on the device and
+ *                    not followed.
+ *   next_order:      device buffer this call fills with the order of the batch whose offsets are
+ *                    next_offsets (NULL = none); it must not overlap tile_order.
+ *   next_offsets:    that batch's offsets, same layout and size as `offsets` (same batch_size and
+ *                    fields); only the offsets are read, while this call runs.
+ *   order_bytes:     size of each order buffer, >= cti_ebag_order_bytes(batch_size, num_fields).
+ * An order applies to jobs whose fields all take the same tiled row shape (one aligned row width),
+ * with at most 64 fields and no binning (CTI_EBAG_EUNSUPPORTED otherwise). Calls that read or
+ * write the same order buffer on different streams race.                                          */
 typedef struct cti_ebag_options {
   int32_t long_threshold;
   int32_t use_bins;
   int32_t block_threshold;
   int32_t split_threshold;
-  int32_t reserved[4];
+  const int32_t* tile_order;
+  int32_t* next_order;
+  const int64_t* next_offsets;
+  int64_t order_bytes;
 } cti_ebag_options;
 
 /* ABI version this library was built with (CTI_EBAG_ABI_VERSION). */
@@ -154,6 +173,11 @@ int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const 
  * (256 + 24 * batch_size * min(num_fields, 64): list counters, then the field / sample and the
  * value range of each listed bag); -1 for negative arguments. */
 int64_t cti_ebag_workspace_bytes(int64_t batch_size, int32_t num_fields);
+
+/* Bytes of each dispatch-order buffer (cti_ebag_options.tile_order / next_order) for any job of
+ * batch_size samples and num_fields fields (16 + 4 * batch_size * min(num_fields, 64)); -1 for
+ * negative arguments. No counterpart in the reference. */
+int64_t cti_ebag_order_bytes(int64_t batch_size, int32_t num_fields);
 
 /*
  * Device packer for the reference flat layout (online_best/infer.py:960-974, and the

@@ -23,7 +23,7 @@ def test_header_declares_the_entry_points():
               "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version", "cti_ebag_layernorm",
               "cti_ebag_fused_all_slots_int8", "cti_ebag_quantize_int8", "cti_ebag_fused_all_slots_typed",
               "cti_ebag_narrow_ids", "cti_ebag_stage_copy", "cti_ebag_stage_offset",
-              "cti_ebag_fused_all_slots_layernorm"):
+              "cti_ebag_fused_all_slots_layernorm", "cti_ebag_order_bytes"):
         assert n in names
 
 
@@ -157,6 +157,51 @@ def test_workspace_query(pkg):
     assert lib.cti_ebag_workspace_bytes(4096, 28) == 256 + 24 * 4096 * 28
     assert lib.cti_ebag_workspace_bytes(10, 100) == 256 + 24 * 10 * 64
     assert lib.cti_ebag_workspace_bytes(-1, 28) < 0
+
+
+def test_order_query(pkg):
+    lib = pkg._capi.lib()
+    assert lib.cti_ebag_order_bytes(4096, 28) == 16 + 4 * 4096 * 28
+    assert lib.cti_ebag_order_bytes(10, 100) == 16 + 4 * 10 * 64
+    assert lib.cti_ebag_order_bytes(-1, 28) < 0
+
+
+def test_options_struct_matches_header(pkg):
+    text = open(HEADER).read()
+    body = re.search(r"typedef struct cti_ebag_options \{(.*?)\} cti_ebag_options;", text, re.S).group(1)
+    fields = re.findall(r"(\w+)\s*;", re.sub(r"/\*.*?\*/", "", body, flags=re.S))
+    assert fields == [f for f, _ in pkg._capi.Options._fields_]
+    assert ctypes.sizeof(pkg._capi.Options) == 48
+
+
+def test_dispatch_order_rejects_bad_arguments(pkg):
+    """Every case fails a host-side check, so nothing is launched (the pointers are not real).
+    One field of bf16 rows of 128 (16 lanes x 8 values, 8 bags per tile), batch 4: one tile."""
+    c = pkg._capi
+
+    def call(tables=None, num_fields=1, out=256, stride=128, ws=None, ws_bytes=0, use_bins=0, **o):
+        opts = c.Options()
+        opts.use_bins = use_bins
+        for k, v in o.items():
+            assert k in dict(c.Options._fields_)
+            setattr(opts, k, v)
+        return _forward(pkg, tables=tables if tables is not None else _table(pkg, data=256), num_fields=num_fields,
+                        out=out, stride=stride, ws=ws, ws_bytes=ws_bytes, opts=ctypes.byref(opts))
+
+    assert call(tile_order=258, order_bytes=1 << 20) == c.EINVAL and "aligned" in c.last_error()
+    assert call(next_order=256, order_bytes=1 << 20) == c.EINVAL and "next_offsets" in c.last_error()
+    assert call(tile_order=256, order_bytes=0) == c.EINVAL
+    assert call(tile_order=256, next_order=264, next_offsets=512, order_bytes=64) == c.EINVAL
+    assert "overlap" in c.last_error()
+    assert call(tile_order=256, order_bytes=19) == c.EINVAL and "20" in c.last_error()  # 4 + 1 entries
+    assert call(tile_order=256, order_bytes=64, use_bins=1, ws=256, ws_bytes=1 << 20) == c.EUNSUPPORTED
+    # a misaligned output takes the generic kernel, which has no dispatch order
+    assert call(tile_order=256, order_bytes=64, out=2) == c.EUNSUPPORTED
+    # two row widths take the mixed-width launch
+    two = (c.Table * 2)()
+    for i, (d, col) in enumerate(((128, 0), (64, 128))):
+        two[i].data, two[i].rows, two[i].row_stride, two[i].dim, two[i].out_col = 256, 100, d, d, col
+    assert call(tables=two, stride=192, num_fields=2, tile_order=256, order_bytes=1 << 10) == c.EUNSUPPORTED
 
 
 def test_binning_requires_a_workspace(pkg):

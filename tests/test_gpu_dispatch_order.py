@@ -1,0 +1,214 @@
+"""Pooling with a dispatch order made one batch ahead (PooledEmbedding(dispatch_order=True); the
+C ABI's cti_ebag_options.tile_order / next_order / next_offsets).
+
+Each call pools its batch and, in eight extra workgroups, sorts the next batch's tiles, most rows
+per bag first within each XCD's share; the next call follows that order. Only the sequence in
+which tiles start changes, so every output must equal the unordered call bit for bit: along a
+stream of batches, when the batch that comes is not the one the order was made for, when the
+order was made for another tile count (not followed), and when a buffer's entries are all out of
+range. The order itself is checked on the host: its header, then each XCD range a permutation of
+itself, sorted by rows per bag in chunks of 2048 tiles. Bags of at most 48 rows are pooled by one
+lane group in element order, so batches without longer bags also match the oracle bit for bit.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from _cases import make_ids, make_table
+from oracle import ebag_oracle as orc
+from test_gpu_parity import to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+MAGIC = 0x4F524452
+CHUNK = 2048
+V = 3000
+
+# (table dtype, dim, fields, batch, max short-bag length, int8 tables, bags per tile)
+SHAPES = [
+    ("bf16", 128, 28, 512, 24, False, 8),   # the bf16 [*, 128] shape of the headline, smaller batch
+    ("f32", 64, 5, 333, 40, False, 8),      # batch not a multiple of the tile
+    ("bf16", 512, 3, 100, 30, False, 2),    # 64 lanes x 1 vector
+    ("f32", 1024, 2, 50, 20, False, 2),     # 64 lanes x 4 vectors
+    ("bf16", 128, 4, 200, 30, True, 8),     # int8 row-quantised tables
+    ("bf16", 128, 1, 5, 48, False, 8),      # one tile: seven XCD ranges are empty
+]
+
+
+def _bits(t):
+    return t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.int16)
+
+
+def _batches(seed, F, B, max_len, n=4):
+    """n batches of one shape: short bags; some long bags; mostly empty; short bags again."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for k in range(n):
+        L = rng.integers(0, max_len + 1, size=(F, B))
+        if k == 1:
+            L[:, ::7] = rng.integers(100, 250, size=L[:, ::7].shape)
+        if k == 2:
+            L[rng.random((F, B)) < 0.7] = 0
+        off = np.zeros(F * B + 1, np.int64)
+        np.cumsum(L.reshape(-1), out=off[1:])
+        out.append((make_ids(rng, int(L.sum()), V), off, int(L.max(initial=0)) <= 48))
+    return out
+
+
+def _setup(pkg, dev, shape, seed):
+    tdt, D, F, B, max_len, int8, _ = SHAPES[shape]
+    rng = np.random.default_rng(seed)
+    host = [make_table(rng, V, D, tdt) for _ in range(F)]
+    tables = [to_dev(t, tdt, dev) for t in host]
+    if int8:
+        tables = [pkg.quantize_embedding_int8(t) for t in tables]
+    odt = torch.float32 if tdt == "f32" else torch.bfloat16
+    plain = pkg.PooledEmbedding(tables, out_dtype=odt)
+    ordered = pkg.PooledEmbedding(tables, out_dtype=odt, dispatch_order=True)
+    batches = _batches(seed + 1, F, B, max_len)
+    dev_batches = [(torch.from_numpy(i).to(dev), torch.from_numpy(o).to(dev)) for i, o, _ in batches]
+    return host, plain, ordered, batches, dev_batches
+
+
+def _check_order(order, off, F, B, NB):
+    """The order buffer made from offsets `off`: header, XCD ranges permuted, chunks sorted."""
+    n = int(order[0])
+    assert order[1] == MAGIC and order[2] == 0 and order[3] == 0
+    tpf = -(-B // NB)
+    assert n == F * tpf
+    t = np.arange(n)
+    fi = t // tpf
+    b0 = (t - fi * tpf) * NB
+    b1 = np.minimum(b0 + NB, B)
+    per_bag = np.clip((off[fi * B + b1] - off[fi * B + b0]) // NB, 0, 63)
+    body = order[4:4 + n]
+    q, r = divmod(n, 8)
+    for x in range(8):
+        lo = x * (q + 1) if x < r else r * (q + 1) + (x - r) * q
+        cnt = q + (1 if x < r else 0)
+        for c0 in range(0, cnt, CHUNK):
+            part = body[lo + c0:lo + min(cnt, c0 + CHUNK)]
+            assert np.array_equal(np.sort(part), np.arange(lo + c0, lo + c0 + len(part))), (x, c0)
+            assert (np.diff(per_bag[part]) <= 0).all(), (x, c0)
+
+
+@pytest.mark.parametrize("shape", range(len(SHAPES)))
+def test_ordered_stream_equals_unordered(pkg, dev, shape):
+    tdt, D, F, B, _, int8, NB = SHAPES[shape]
+    host, plain, ordered, batches, dev_batches = _setup(pkg, dev, shape, 700 + 10 * shape)
+    n = len(dev_batches)
+    for rep in range(2):
+        for k, (v, o) in enumerate(dev_batches):
+            # first pass: the batch that comes next; second pass: another one (a wrong guess)
+            nk = k + 1 if rep == 0 else (k + 2) % n
+            nxt = dev_batches[nk][1] if k + 1 < n else None
+            got = ordered(v, o, next_offsets=nxt)
+            if nxt is not None:
+                _check_order(ordered._orders[ordered._cur].cpu().numpy(), batches[nk][1], F, B, NB)
+            want = plain(v, o)
+            torch.cuda.synchronize()
+            assert torch.equal(_bits(got), _bits(want)), (rep, k)
+            if rep == 0 and not int8 and batches[k][2]:
+                odt = "f32" if tdt == "f32" else "bf16"
+                ref = orc.pool_c(batches[k][0], batches[k][1], host, tdt, "sum", odt)
+                assert np.array_equal(to_np(got, odt), ref), k
+
+
+@pytest.mark.parametrize("F,D,B,NB", [(28, 128, 4096, 8), (64, 512, 4096, 2)])
+def test_order_of_full_size_batches(pkg, dev, F, D, B, NB):
+    # 28 x 4096 bags of bf16 [*, 128] rows: 14,336 tiles, one chunk per XCD range;
+    # 64 x 4096 bags of bf16 [*, 512] rows: 131,072 tiles, eight chunks per XCD range
+    rng = np.random.default_rng(F + D)
+    tables = [to_dev(make_table(rng, 500, D, "bf16"), "bf16", dev) for _ in range(F)]
+    plain = pkg.PooledEmbedding(tables)
+    ordered = pkg.PooledEmbedding(tables, dispatch_order=True)
+    batches = []
+    for _ in range(3):
+        L = np.minimum(rng.geometric(1 / 9, size=(F, B)) - 1, 256)
+        off = np.zeros(F * B + 1, np.int64)
+        np.cumsum(L.reshape(-1), out=off[1:])
+        ids = make_ids(rng, int(off[-1]), 500)
+        batches.append((off, torch.from_numpy(ids).to(dev), torch.from_numpy(off).to(dev)))
+    for k in range(3):
+        _, v, o = batches[k]
+        nxt = batches[k + 1] if k + 1 < 3 else None
+        got = ordered(v, o, next_offsets=nxt[2] if nxt else None)
+        if nxt:
+            _check_order(ordered._orders[ordered._cur].cpu().numpy(), nxt[0], F, B, NB)
+        want = plain(v, o)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(got), _bits(want)), k
+
+
+def _forward(pkg, plan, v, o, out, tile_order=None, next_order=None, next_offsets=None, order_bytes=0):
+    c = pkg._capi
+    opts = c.Options()
+    opts.tile_order, opts.next_order, opts.next_offsets, opts.order_bytes = tile_order, next_order, next_offsets, \
+        order_bytes
+    batch = (o.numel() - 1) // plan.num_fields
+    return c.lib().cti_ebag_forward(v.data_ptr(), c.I64, v.numel(), o.data_ptr(), batch, plan.num_fields, plan._descs,
+                                    plan._tdt, plan._pool, out.data_ptr(), plan._odt, plan.width, None, 0,
+                                    ctypes.byref(opts), torch.cuda.current_stream().cuda_stream)
+
+
+def test_orders_for_other_launches_are_not_followed(pkg, dev):
+    c = pkg._capi
+    F, D, V_ = 6, 128, 400
+    rng = np.random.default_rng(77)
+    tables = [to_dev(make_table(rng, V_, D, "bf16"), "bf16", dev) for _ in range(F)]
+    plain = pkg.PooledEmbedding(tables)
+
+    def batch(B):
+        L = rng.integers(0, 40, size=(F, B))
+        L[:, ::5] = 200
+        off = np.zeros(F * B + 1, np.int64)
+        np.cumsum(L.reshape(-1), out=off[1:])
+        return torch.from_numpy(make_ids(rng, int(off[-1]), V_)).to(dev), torch.from_numpy(off).to(dev)
+
+    small, big = batch(150), batch(300)
+    nbytes = c.lib().cti_ebag_order_bytes(300, F)
+    bufs = [torch.zeros(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(2)]
+    out = torch.empty((300, F * D), dtype=torch.bfloat16, device=dev)
+    want_small, want_big = plain(*small), plain(*big)
+    # the small batch makes an order for a small batch (19 tiles per field) ...
+    out_s = torch.empty((150, F * D), dtype=torch.bfloat16, device=dev)
+    assert _forward(pkg, plain, *small, out_s, None, bufs[0].data_ptr(), small[1].data_ptr(), nbytes) == c.OK
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out_s), _bits(want_small))
+    assert bufs[0][0].item() == F * 19 and bufs[0][1].item() == MAGIC
+    # ... which the big batch (38 tiles per field) does not follow
+    assert _forward(pkg, plain, *big, out, bufs[0].data_ptr(), None, None, nbytes) == c.OK
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out), _bits(want_big))
+    # a zeroed buffer, and one with the right header but every entry out of range
+    for fill in (0, -1):
+        bufs[1].fill_(fill)
+        if fill:
+            bufs[1][0], bufs[1][1] = F * 38, MAGIC
+        out.zero_()
+        assert _forward(pkg, plain, *big, out, bufs[1].data_ptr(), None, None, nbytes) == c.OK
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(out), _bits(want_big)), fill
+
+
+def test_python_plan_rejects_what_it_cannot_order(pkg, dev):
+    rng = np.random.default_rng(5)
+    t128 = to_dev(make_table(rng, 100, 128, "bf16"), "bf16", dev)
+    t64 = to_dev(make_table(rng, 100, 64, "bf16"), "bf16", dev)
+    with pytest.raises(ValueError, match="use_bins"):
+        pkg.PooledEmbedding([t128], dispatch_order=True, use_bins=True, max_batch=8)
+    off = torch.arange(9, dtype=torch.int64, device=dev)
+    ids = torch.zeros(8, dtype=torch.int64, device=dev)
+    with pytest.raises(ValueError, match="dispatch_order"):
+        pkg.PooledEmbedding([t128])(ids, off, next_offsets=off)
+    plan = pkg.PooledEmbedding([t128], dispatch_order=True)
+    with pytest.raises(ValueError, match="next_offsets"):
+        plan(ids, off, next_offsets=off[:5])
+    # fields of two widths take the mixed-width launch, which has no dispatch order
+    mixed = pkg.PooledEmbedding([t128, t64], dispatch_order=True)
+    off2 = torch.arange(17, dtype=torch.int64, device=dev)
+    ids2 = torch.zeros(16, dtype=torch.int64, device=dev)
+    with pytest.raises(pkg._capi.EbagError):
+        mixed(ids2, off2, next_offsets=off2)
