@@ -515,8 +515,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # 300 untimed steps (~12 ms): the first ~10 ms of sustained load run 1-3 us per step slower
-    ap.add_argument("--warmup", type=int, default=300)
+    # 1000 untimed steps (~37 ms): the first ~10-30 ms of sustained load run 0.5-3 us per step slower
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--workload", default="bf16-2m", choices=sorted(WORKLOAD_TEXT))
     ap.add_argument("--sets", type=int, default=8, help="independently seeded index sets rotated over")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
