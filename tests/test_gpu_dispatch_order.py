@@ -212,3 +212,40 @@ def test_python_plan_rejects_what_it_cannot_order(pkg, dev):
     ids2 = torch.zeros(16, dtype=torch.int64, device=dev)
     with pytest.raises(pkg._capi.EbagError):
         mixed(ids2, off2, next_offsets=off2)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_shapes_ordered_equal_unordered(pkg, dev, seed):
+    # one row width per case (the order needs one tiled row shape): any width and dtype; widths
+    # that are not whole 16-byte vectors take the generic kernel, which must refuse the order
+    rng = np.random.default_rng(9000 + seed)
+    tdt = ["f32", "bf16", "f16"][seed % 3]
+    D = int(rng.choice([1, 4, 8, 16, 24, 32, 64, 96, 128, 256, 512, 1024]))
+    F, B = int(rng.integers(1, 41)), int(rng.integers(1, 601))
+    Vs = int(rng.integers(1, 3000))
+    tables = [to_dev(make_table(rng, Vs, D, tdt), tdt, dev) for _ in range(F)]
+    odt = [torch.float32, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
+    plain = pkg.PooledEmbedding(tables, out_dtype=odt, pooling=["sum", "mean"][seed % 2])
+    ordered = pkg.PooledEmbedding(tables, out_dtype=odt, pooling=["sum", "mean"][seed % 2], dispatch_order=True)
+    batches = []
+    for k in range(3):
+        L = rng.integers(0, int(rng.integers(1, 80)) + 1, size=(F, B))
+        if k == 1:
+            L[:, ::int(rng.integers(2, 9))] = int(rng.integers(50, 400))
+        off = np.zeros(F * B + 1, np.int64)
+        np.cumsum(L.reshape(-1), out=off[1:])
+        batches.append((torch.from_numpy(make_ids(rng, int(off[-1]), Vs)).to(dev), torch.from_numpy(off).to(dev)))
+    # the tiled kernels take rows of 1, 2, 4, ..., 64, 128 or 256 whole 16-byte vectors
+    row_bytes = D * (4 if tdt == "f32" else 2)
+    tiled = row_bytes % 16 == 0 and row_bytes // 16 in {1, 2, 4, 8, 16, 32, 64, 128, 256}
+    try:
+        for k, (v, o) in enumerate(batches):
+            got = ordered(v, o, next_offsets=batches[k + 1][1] if k + 1 < len(batches) else None)
+            want = plain(v, o)
+            torch.cuda.synchronize()
+            assert torch.equal(_bits(got) if got.element_size() == 4 else got.view(torch.int16),
+                               _bits(want) if want.element_size() == 4 else want.view(torch.int16)), k
+    except pkg._capi.EbagError as e:
+        assert not tiled and e.status == pkg._capi.EUNSUPPORTED, e  # refused before any launch
+    else:
+        assert tiled, "a job of the generic kernel took a dispatch order"
