@@ -75,17 +75,62 @@ def log(msg):
 
 def traffic_from_profiles(workload, kernel="pool_kernel", keys=("hbm_bytes_per_launch",)):
     """HBM bytes per launch recorded by the rocprofv3 counter runs, read from the first of the
-    lines `<key>: N` (in the order of `keys`) of profiles/<kernel>_<workload>.md, or None."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}.md")
+    lines `<key>: N` (in the order of `keys`) of profiles/<kernel>_<workload>.md, as
+    (bytes, "profiles/<file>") or (None, None)."""
+    name = f"{kernel}_{workload}.md"
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as fh:
         lines = [line.strip() for line in fh]
     for key in keys:
         for line in lines:
             if line.startswith(key + ":"):
-                return float(line.split(":", 1)[1].strip())
-    return None
+                return float(line.split(":", 1)[1].strip()), f"profiles/{name}"
+    return None, None
+
+
+def roofline(achieved_gbs, nbytes, launch_s, kernel, traffic_key=None, **extra):
+    """The bench line's roofline object. `achieved` is algorithmic bytes / mean launch time;
+    `dram_frac` is the HBM traffic the counters measured for one launch of the same kernel and
+    workload (`traffic`, from `traffic_source`) moved in the mean launch time, against the peak."""
+    traffic, source = traffic_from_profiles(*traffic_key) if traffic_key else (None, None)
+    rec = {"bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic,
+           "dram_frac": traffic / launch_s / 1e9 / HBM_PEAK_GBS if traffic else None,
+           "traffic_source": source, "kernel": kernel, "bytes_per_launch": nbytes, "launch_us_mean": launch_s * 1e6}
+    rec.update(extra)
+    return rec
+
+
+def host_cpus():
+    """The host's CPU counts: logical CPUs, the ones this process may run on, physical cores, and
+    the CPU share its cgroup grants (cpu.max quota / period), when these are visible."""
+    info = {"logical": os.cpu_count()}
+    try:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["affinity"] = info["logical"]
+    try:
+        import psutil
+
+        info["physical"] = psutil.cpu_count(logical=False)
+    except Exception:  # psutil missing or unable to read the topology
+        info["physical"] = None
+    info["cgroup_share"] = None
+    for path in ("/sys/fs/cgroup/cpu.max", "/sys/fs/cgroup/cpu/cpu.cfs_quota_us"):
+        try:
+            with open(path) as fh:
+                parts = fh.read().split()
+            if path.endswith("cpu.max") and parts[0] != "max":
+                info["cgroup_share"] = float(parts[0]) / float(parts[1])
+            elif path.endswith("quota_us") and int(parts[0]) > 0:
+                with open("/sys/fs/cgroup/cpu/cpu.cfs_period_us") as fh:
+                    info["cgroup_share"] = int(parts[0]) / int(fh.read())
+            break
+        except (OSError, ValueError, IndexError):
+            continue
+    return info
 
 
 def cpu_baseline(wl, tables_dev, seconds):
@@ -99,7 +144,12 @@ def cpu_baseline(wl, tables_dev, seconds):
 
     from oracle import cpu_loops
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    cpus = host_cpus()
+    # every CPU this process may run on, capped by the CPU share its cgroup grants (threads beyond
+    # the share only queue for it)
+    threads = cpus["affinity"] or 1
+    if cpus["cgroup_share"]:
+        threads = max(1, min(threads, int(cpus["cgroup_share"])))
     torch.set_num_threads(threads)
     host = []
     for f, t in enumerate(tables_dev):
@@ -127,9 +177,11 @@ def cpu_baseline(wl, tables_dev, seconds):
     med_bag, n_bag, el_bag = timed(cpu_loops.embedding_bag_loop)
     med_lit, n_lit, el_lit = timed(cpu_loops.baseline_loop)
     return {"value": wl.num_bags / med_bag, "unit": "bags/s", "cores": threads, "kind": "port",
+            "host_logical_cpus": cpus["logical"], "host_physical_cores": cpus["physical"],
+            "process_affinity_cpus": cpus["affinity"], "cgroup_cpu_share": cpus["cgroup_share"],
             "sample": f"median of {n_bag} full passes ({el_bag:.1f} s) of the timed batch ({wl.num_bags} bags) "
                       f"through F.embedding_bag per field (oracle/cpu_loops.py), {wl.table_dtype} tables in host "
-                      f"memory",
+                      f"memory, torch intra-op threads = {threads}",
             "baseline_loop": {"value": wl.num_bags / med_lit, "unit": "bags/s",
                               "sample": f"median of {n_lit} passes ({el_lit:.1f} s) of the literal loop: clamp + "
                                         "F.embedding + segment_reduce + cat (baseline/infer.py:256-263)"}}
@@ -310,11 +362,8 @@ def bench_encoder(args, pkg, wls, dev):
         "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}; reference layout, one shared "
                                "table, sum pooling, then LayerNorm over [B, 28*128]"},
         "us_per_step": {"pool_then_layernorm": t_sep * 1e6, "fused": t_fused * 1e6},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic_from_profiles(args.workload + "-shared", "pool_norm_kernel"),
-                     "kernel": "pool_norm_kernel",
-                     "bytes_per_launch": fused_bytes, "launch_us_mean": t_fused * 1e6},
+        "roofline": roofline(achieved, fused_bytes, t_fused, "pool_norm_kernel",
+                             (args.workload + "-shared", "pool_norm_kernel")),
         "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
@@ -456,10 +505,8 @@ def bench_layout(args, pkg, dev):
                         "reference_pack": wall_ref_pack * 1e6, "reference_pack_gpu": k_ref_pack * 1e6,
                         "device_pack_python": wall_pack * 1e6, "device_pack_raw": wall_pack_raw * 1e6,
                         "device_pack_gpu": k_pack * 1e6},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "merge_kernel",
-                     "bytes_per_launch": merge_bytes, "launch_us_mean": k_merge * 1e6,
-                     "pack_bytes_per_launch": pack_bytes, "pack_achieved": pack_bytes / k_pack / 1e9},
+        "roofline": roofline(achieved, merge_bytes, k_merge, "merge_kernel", None,
+                             pack_bytes_per_launch=pack_bytes, pack_achieved=pack_bytes / k_pack / 1e9),
         "cpu_baseline": {"value": lazy.batch * F / t_ref_merge, "unit": "bags/s", "cores": torch.get_num_threads(),
                          "kind": "port", "sample": "the reference merge (torch ops on host tensors) of the same "
                                                    "8 sub-batches, repeated for 3 s"},
@@ -503,9 +550,7 @@ def bench_layernorm(args, pkg, plan, inputs, wl0, dev):
         "data": "synthetic: pooled blocks of 4 seeded index sets rotated",
         "config": {"workload": f"layernorm over the pooled {args.workload} block", "rows": blocks[0].shape[0],
                    "cols": width},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "norm_rows_kernel",
-                     "bytes_per_launch": nbytes, "launch_us_mean": launch_s * 1e6},
+        "roofline": roofline(achieved, nbytes, launch_s, "norm_rows_kernel", None),
         "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
@@ -674,15 +719,11 @@ def main():
                    "nnz_mean": float(np.mean([wl.nnz for wl in wls])), "index_sets": args.sets,
                    "length_binning": bool(args.bins), "int8_tables": bool(args.int8),
                    "dispatch_order": bool(args.dispatch_order)},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic_from_profiles(
-                         args.workload + ("-int8" if args.int8 else ""), prof_kernel,
-                         ("hbm_bytes_per_launch",) if args.dispatch_order
-                         else ("hbm_bytes_per_launch_order_off", "hbm_bytes_per_launch")),
-                     "kernel": kernel_name,
-                     "bytes_per_launch": used_bytes,
-                     "compulsory_bytes_per_launch": used_comp, "launch_us_mean": mean_launch_s * 1e6},
+        "roofline": roofline(achieved, used_bytes, mean_launch_s, kernel_name,
+                             (args.workload + ("-int8" if args.int8 else ""), prof_kernel,
+                              ("hbm_bytes_per_launch",) if args.dispatch_order
+                              else ("hbm_bytes_per_launch_order_off", "hbm_bytes_per_launch")),
+                             compulsory_bytes_per_launch=used_comp),
         "cpu_baseline": cpu,
     }
     if accuracy is not None:

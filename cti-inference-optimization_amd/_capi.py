@@ -94,6 +94,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_PP, _PP, _PP, _PI64, _PI64, _I32, _I32, _P, _P, _P, _P, _P],
     ),
+    "cti_ebag_merge_batches_int32": (
+        ctypes.c_int,
+        [_PP, _PP, _PP, _PI64, _PI64, _I32, _I32, _P, _P, _P, _P, _P],
+    ),
     "cti_ebag_layernorm": (
         ctypes.c_int,
         [_P, _P, _I64, _I64, _I32, _P, _P, _I32, ctypes.c_float, _P, _P, _P],

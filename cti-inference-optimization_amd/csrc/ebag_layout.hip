@@ -25,19 +25,25 @@ struct __attribute__((aligned(8))) I64Pair {
   int64_t a, b;
 };
 
-// dst[i] = src[i] + add for i < n; grid-stride item j covers elements 2j and 2j+1.
+// x, or with `wrap` the int64 value of its low 32 bits read as int32 (torch's .int().long()).
+__device__ __forceinline__ int64_t wrap32(int64_t x, bool wrap) {
+  return wrap ? static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(static_cast<uint64_t>(x)))) : x;
+}
+
+// dst[i] = post + wrap32(src[i] + add) for i < n; grid-stride item j covers elements 2j and 2j+1.
 __device__ __forceinline__ void copy_add_i64(const int64_t* __restrict__ src, int64_t* __restrict__ dst, int64_t n,
-                                             int64_t add, int64_t j0, int64_t stride) {
+                                             int64_t add, int64_t j0, int64_t stride, bool wrap = false,
+                                             int64_t post = 0) {
   for (int64_t j = j0; 2 * j < n; j += stride) {
     const int64_t e = 2 * j;
     if (e + 1 < n) {
       I64Pair v;
       __builtin_memcpy(&v, src + e, sizeof(v));
-      v.a += add;
-      v.b += add;
+      v.a = post + wrap32(v.a + add, wrap);
+      v.b = post + wrap32(v.b + add, wrap);
       __builtin_memcpy(dst + e, &v, sizeof(v));
     } else {
-      dst[e] = src[e] + add;
+      dst[e] = post + wrap32(src[e] + add, wrap);
     }
   }
 }
@@ -92,6 +98,7 @@ struct MergeParams {
   int64_t batch;
   int32_t num_sub;
   int32_t num_slots;
+  int32_t wrap32;  // the pair merge's int32 round trip of values and row offsets
 };
 
 // Slot s of sub-batch k: values [slot_start, slot_start + slot_nnz), its val_offsets entries
@@ -163,15 +170,18 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const MergeParams p) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kThreads + t;
   const int64_t* __restrict__ so = p.ro[k] + static_cast<int64_t>(s) * (Bk + 1);
-  copy_add_i64(p.vals[k] + src0, p.flat_values + dst0, n, 0, i0, stride);
-  copy_add_i64(so, p.flat_row_offsets + static_cast<int64_t>(s) * (B + 1) + p.bbase[k], Bk, vb, i0, stride);
+  const bool w = p.wrap32 != 0;
+  copy_add_i64(p.vals[k] + src0, p.flat_values + dst0, n, 0, i0, stride, w);
+  copy_add_i64(so, p.flat_row_offsets + static_cast<int64_t>(s) * (B + 1) + p.bbase[k], Bk, vb, i0, stride, w);
+  // global form: slot base + the (possibly wrapped) slot-local offset, as a reader of the merged
+  // flat layout would add them
   if (p.global_offsets)
-    copy_add_i64(so, p.global_offsets + static_cast<int64_t>(s) * B + p.bbase[k], Bk, before + vb, i0, stride);
+    copy_add_i64(so, p.global_offsets + static_cast<int64_t>(s) * B + p.bbase[k], Bk, vb, i0, stride, w, before);
   if (i0 == 0) {
-    if (k == K - 1) p.flat_row_offsets[static_cast<int64_t>(s) * (B + 1) + B] = tot;
+    if (k == K - 1) p.flat_row_offsets[static_cast<int64_t>(s) * (B + 1) + B] = wrap32(tot, w);
     if (k == 0) p.val_offsets[s] = before;
     if (p.global_offsets && k == 0 && s == p.num_slots - 1)
-      p.global_offsets[static_cast<int64_t>(p.num_slots) * B] = before + tot;
+      p.global_offsets[static_cast<int64_t>(p.num_slots) * B] = before + wrap32(tot, w);
   }
 }
 
@@ -235,12 +245,13 @@ extern "C" int cti_ebag_pack_slots(const int64_t* const* slot_values, const int6
   return CTI_EBAG_OK;
 }
 
-extern "C" int cti_ebag_merge_batches(const int64_t* const* sub_values, const int64_t* const* sub_val_offsets,
-                                      const int64_t* const* sub_row_offsets, const int64_t* sub_batch,
-                                      const int64_t* sub_nnz, int32_t num_sub, int32_t num_slots,
-                                      int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
-                                      int64_t* global_offsets, void* stream) {
-  clear_error();
+namespace cti {
+namespace {
+
+int merge(const int64_t* const* sub_values, const int64_t* const* sub_val_offsets,
+          const int64_t* const* sub_row_offsets, const int64_t* sub_batch, const int64_t* sub_nnz, int32_t num_sub,
+          int32_t num_slots, int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
+          int64_t* global_offsets, bool wrap32, void* stream) {
   if (num_sub < 0 || num_slots < 0) return set_error(CTI_EBAG_EINVAL, "num_sub and num_slots must be >= 0");
   if (num_sub == 0 || num_slots == 0) return CTI_EBAG_OK;
   if (num_sub > kMaxSub) return set_error(CTI_EBAG_EUNSUPPORTED, "at most %d sub-batches per merge (got %d)", kMaxSub, num_sub);
@@ -275,8 +286,32 @@ extern "C" int cti_ebag_merge_batches(const int64_t* const* sub_values, const in
   p.batch = B;
   p.num_sub = num_sub;
   p.num_slots = num_slots;
+  p.wrap32 = wrap32 ? 1 : 0;
   const int64_t per_slot = (longest + num_slots - 1) / num_slots;
   const dim3 grid(static_cast<unsigned>(chunks_for(per_slot, 256)), static_cast<unsigned>(num_slots * num_sub));
   hipLaunchKernelGGL(merge_kernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), p);
   return check_launch("cti_ebag_merge_batches");
+}
+
+}  // namespace
+}  // namespace cti
+
+extern "C" int cti_ebag_merge_batches(const int64_t* const* sub_values, const int64_t* const* sub_val_offsets,
+                                      const int64_t* const* sub_row_offsets, const int64_t* sub_batch,
+                                      const int64_t* sub_nnz, int32_t num_sub, int32_t num_slots,
+                                      int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
+                                      int64_t* global_offsets, void* stream) {
+  clear_error();
+  return merge(sub_values, sub_val_offsets, sub_row_offsets, sub_batch, sub_nnz, num_sub, num_slots, flat_values,
+               flat_row_offsets, val_offsets, global_offsets, false, stream);
+}
+
+extern "C" int cti_ebag_merge_batches_int32(const int64_t* const* sub_values, const int64_t* const* sub_val_offsets,
+                                            const int64_t* const* sub_row_offsets, const int64_t* sub_batch,
+                                            const int64_t* sub_nnz, int32_t num_sub, int32_t num_slots,
+                                            int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
+                                            int64_t* global_offsets, void* stream) {
+  clear_error();
+  return merge(sub_values, sub_val_offsets, sub_row_offsets, sub_batch, sub_nnz, num_sub, num_slots, flat_values,
+               flat_row_offsets, val_offsets, global_offsets, true, stream);
 }

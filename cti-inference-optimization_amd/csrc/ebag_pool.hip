@@ -23,7 +23,7 @@
 //     Single-wavefront workgroups need no workgroup barrier, so a wavefront retires as soon as its
 //     own bags are done (measured: multi-wavefront workgroups are slower, also when they share a
 //     length ranking). Row ids are clamped, narrowed to 32 bits (tables have < 2^31 rows) and
-//     broadcast through LDS; a step reads ROWS_IN_FLIGHT ids, then issues that many row loads
+//     broadcast through LDS; a step reads kRowsInFlight ids, then issues that many row loads
 //     before consuming any. A bag's ids are loaded one chunk ahead, so the next chunk's id load
 //     completes under the current chunk's row loads. Tables under 4 GiB with power-of-two row sizes are read with buffer
 //     loads: a row's offset is one shift-add, and rows past a bag's end use an out-of-range offset
@@ -66,22 +66,12 @@
 namespace cti {
 namespace {
 
-// Tuning knobs (compile-time). Defaults are the measured best on MI355X for D=128 bf16.
-#ifndef CTI_EBAG_ROWS_IN_FLIGHT
-#define CTI_EBAG_ROWS_IN_FLIGHT 4  // row vector loads in flight per lane before they are consumed
-#endif
-#ifndef CTI_EBAG_XCD_REMAP
-#define CTI_EBAG_XCD_REMAP 1  // give each XCD a contiguous range of tiles
-#endif
-#ifndef CTI_EBAG_NT_ROWS
-#define CTI_EBAG_NT_ROWS 0  // non-temporal hint on table-row loads
-#endif
-#ifndef CTI_EBAG_ROUNDS
-#define CTI_EBAG_ROUNDS 2  // rounds of R length-ranked bags per tile of the main kernel
-#endif
-#ifndef CTI_EBAG_ID_PREFETCH
-#define CTI_EBAG_ID_PREFETCH 1  // load a bag's next chunk of row ids while the current chunk's rows load
-#endif
+// Measured constants (MI355X, 28 x 4096 bags of bf16 rows of 128):
+//   row loads in flight per lane before they are consumed: 1 / 2 / 4 / 8 / 16 ran 86.7 / 66.3 /
+//   56.3 / 58.4 / 68.1 us on an early build (8 against 4 later: 44.8 against 44.3);
+//   rounds of R length-ranked bags per tile: 2 / 3 / 4 ran 41.7 / 42.5 / 42.1 us.
+constexpr int kRowsInFlight = 4;
+constexpr int kRounds = 2;
 
 constexpr int kMainThreads = kWave;  // main kernel: one wavefront per workgroup
 constexpr int kBinThreads = 256;
@@ -89,21 +79,11 @@ constexpr int64_t kLongBlocksMax = 1024;  // workgroups of the long kernel (they
 constexpr int kMaxFields = 64;
 constexpr int64_t kNoLimit = INT64_MAX;
 
-__device__ __forceinline__ uint4 load_row16(const char* p) {
-#if CTI_EBAG_NT_ROWS
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
-#else
-  return load16(p);
-#endif
-}
-
 // One lane's row vector (Elem<TT>::kVecBytes bytes; an 8-byte vector fills .x and .y).
 template <typename TT>
 __device__ __forceinline__ uint4 load_row_vec(const char* p) {
   if constexpr (Elem<TT>::kVecBytes == 16) {
-    return load_row16(p);
+    return load16(p);
   } else {
     const uint2 v = *reinterpret_cast<const uint2*>(p);
     return make_uint4(v.x, v.y, 0u, 0u);
@@ -161,6 +141,8 @@ struct PoolParams {
   int32_t idx32;
   int32_t off32;            // offsets and val_base are int32 (else int64)
   int32_t buffer_ok;        // every field's span_bytes is set: rows are read with buffer loads
+  int32_t round_bf16;       // int8 tables: round each result to bf16 before the output type (the
+                            // reference's int8 kernel stores acc.to(bfloat16), online_best/infer.py:941)
   FieldDesc f[kMaxFields];
 };
 
@@ -190,16 +172,22 @@ __device__ __forceinline__ int xcd_contiguous(int bid, int n) {
 }
 
 // Tile position of dispatch position `pos` in a launch of n tiles.
-__device__ __forceinline__ int xcd_position(int pos, int n) {
-#if CTI_EBAG_XCD_REMAP
-  return xcd_contiguous(pos, n);
-#else
-  return pos;
-#endif
-}
+__device__ __forceinline__ int xcd_position(int pos, int n) { return xcd_contiguous(pos, n); }
 
 __device__ __forceinline__ int block_tile() {
   return xcd_position(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+}
+
+// int8 tables of the reference-layout entry points: the pooled value as the reference's int8
+// kernel leaves it, rounded to bf16 (round to nearest even) whatever the output type.
+template <typename TT, int N>
+__device__ __forceinline__ void round_like_reference(const PoolParams& p, float* r) {
+  if constexpr (Quantized<TT>::value) {
+    if (p.round_bf16) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) r[i] = __uint_as_float(pack_bf16x2(r[i], 0.f) << 16);
+    }
+  }
 }
 
 // Buffer resource over one table: 32-bit byte offsets, offsets at or past the span read as zeros.
@@ -252,7 +240,7 @@ struct Shape {
   static constexpr int VEC = VB / Elem<TT>::kBytes;  // elements per lane vector
   static constexpr int NACC = VPL * VEC;             // fp32 accumulators per lane
   static constexpr int D = LANES * NACC;             // row width
-  static constexpr int U0 = CTI_EBAG_ROWS_IN_FLIGHT / VPL > 0 ? CTI_EBAG_ROWS_IN_FLIGHT / VPL : 1;
+  static constexpr int U0 = kRowsInFlight / VPL > 0 ? kRowsInFlight / VPL : 1;
   static constexpr int U = U0 < LANES ? U0 : LANES;  // rows per subgroup per step
 };
 
@@ -267,17 +255,11 @@ __device__ __forceinline__ void wave_slice_partial(const PoolParams& p, const ch
   using S = Shape<TT, LANES, VPL>;
   const int lane = lane_id();
   const int g = lane / LANES, sl = lane % LANES;
-#if CTI_EBAG_ID_PREFETCH
   int64_t next_id = s0 + lane < s1 ? load_index(p, s0 + lane) : 0;
-#endif
   for (int64_t c = s0; c < s1; c += kWave) {
-#if CTI_EBAG_ID_PREFETCH
     // ids one chunk ahead: the next chunk's id load overlaps this chunk's row loads
     const int64_t id = next_id;
     if (c + kWave + lane < s1) next_id = load_index(p, c + kWave + lane);
-#else
-    const int64_t id = c + lane < s1 ? load_index(p, c + lane) : 0;
-#endif
     ids[lane] = c + lane < s1 ? static_cast<unsigned int>(clamp_i64(id, 0, max_row)) : 0u;
     const int n = static_cast<int>(s1 - c < kWave ? s1 - c : kWave);
     for (int k = 0; k < n; k += S::U * S::R) {
@@ -317,6 +299,7 @@ __device__ __forceinline__ void store_bag(const PoolParams& p, int64_t b, int ou
 #pragma unroll
   for (int i = 0; i < S::NACC; ++i) r[i] = a[i];
   if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<S::NACC>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
+  round_like_reference<TT, S::NACC>(p, r);
   OT* o = reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col;
 #pragma unroll
   for (int q = 0; q < VPL; ++q) store_out<S::VEC>(o + (q * LANES + sl) * S::VEC, r + q * S::VEC);
@@ -357,7 +340,7 @@ __device__ __forceinline__ void add_step(float* acc, const uint4 (&v)[Shape<TT, 
 template <typename TT, int LANES, int VPL>
 struct TileShape {
   static constexpr int R = kWave / LANES;
-  static constexpr int ROUNDS = CTI_EBAG_ROUNDS * R <= kWave ? CTI_EBAG_ROUNDS : kWave / R;
+  static constexpr int ROUNDS = kRounds * R <= kWave ? kRounds : kWave / R;
   static constexpr int NB = R * ROUNDS;  // bags per tile
 };
 
@@ -443,18 +426,12 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int fi, int local
     float acc[S::NACC];
 #pragma unroll
     for (int i = 0; i < S::NACC; ++i) acc[i] = 0.f;
-#if CTI_EBAG_ID_PREFETCH
     int64_t next_id = sl < Lb ? load_index(p, bs + sl) : 0;
-#endif
     for (int c = 0; __ballot(c < Lb) != 0; c += LANES) {
-#if CTI_EBAG_ID_PREFETCH
       // this chunk's id was loaded one chunk ahead; the next chunk's id load is issued now, so
       // it completes under this chunk's row loads instead of costing its own round trip
       const int64_t id = next_id;
       if (c + LANES + sl < Lb) next_id = load_index(p, bs + c + LANES + sl);
-#else
-      const int64_t id = c + sl < Lb ? load_index(p, bs + c + sl) : 0;
-#endif
       __syncthreads();  // orders this chunk's LDS writes after the last reads
       s.ids[lane] = c + sl < Lb ? static_cast<unsigned int>(clamp_i64(id, 0, max_row)) : r_pad;
       __syncthreads();
@@ -1016,16 +993,10 @@ __device__ __forceinline__ void wave_slice_partial_rt(const PoolParams& p, int f
   const int lane = lane_id();
   const int R = kWave >> ll;  // lane groups; U * R divides 64, so every row slot e below is < 64
   const int g = lane >> ll, sl = lane & ((1 << ll) - 1);
-#if CTI_EBAG_ID_PREFETCH
   int64_t next_id = s0 + lane < s1 ? load_index(p, s0 + lane) : 0;
-#endif
   for (int64_t c = s0; c < s1; c += kWave) {
-#if CTI_EBAG_ID_PREFETCH
     const int64_t id = next_id;
     if (c + kWave + lane < s1) next_id = load_index(p, c + kWave + lane);
-#else
-    const int64_t id = c + lane < s1 ? load_index(p, c + lane) : 0;
-#endif
     ids[lane] = c + lane < s1 ? static_cast<unsigned int>(clamp_i64(id, 0, max_row)) : 0u;
     const int n = static_cast<int>(s1 - c < kWave ? s1 - c : kWave);
     for (int k = 0; k < n; k += U * R) {
@@ -1058,6 +1029,7 @@ __device__ __forceinline__ void store_bag_rt(const PoolParams& p, int64_t b, int
 #pragma unroll
   for (int i = 0; i < VEC; ++i) r[i] = a[i];
   if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<VEC>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
+  round_like_reference<TT, VEC>(p, r);
   store_out<VEC>(reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col + sl * VEC, r);
 }
 
@@ -1221,6 +1193,7 @@ __global__ void __launch_bounds__(kMainThreads) pool_generic_kernel(const PoolPa
       if (col < dim) {
         float r = acc[i];
         if (p.pooling == CTI_EBAG_MEAN && L > 0) r = r / static_cast<float>(L);
+        round_like_reference<TT, 1>(p, &r);
         store_one(o + col, r);
       }
     }
@@ -1234,16 +1207,14 @@ int lanes_of(int variant) { return variant <= 6 ? (1 << variant) : 64; }
 int bags_per_tile(int variant) {
   if (variant == kVarGeneric) return 1;
   const int r = kWave / lanes_of(variant);
-  return CTI_EBAG_ROUNDS * r <= kWave ? CTI_EBAG_ROUNDS * r : kWave;  // as TileShape::NB
+  return kRounds * r <= kWave ? kRounds * r : kWave;  // as TileShape::NB
 }
 
-#ifndef CTI_EBAG_SUB_THRESHOLD
-#define CTI_EBAG_SUB_THRESHOLD 48  // default: longer bags are split over the wavefront's subgroups
-#endif
+constexpr int64_t kSubThreshold = 48;  // default: longer bags are split over the wavefront's subgroups
 
 int64_t default_sub_threshold(int variant) {
   if (variant == kVarGeneric) return kNoLimit;  // the element-wise kernel never splits
-  return CTI_EBAG_SUB_THRESHOLD;
+  return kSubThreshold;
 }
 
 // With binning, bags longer than this go to the long kernel.
@@ -1379,6 +1350,7 @@ struct Job {
   int32_t* next_order;        // optional: make the next batch's order here
   const void* next_offsets;
   int64_t order_bytes;        // size of each order buffer
+  int32_t round_bf16;         // int8 tables: results rounded to bf16 before the output type
 };
 
 int validate_tables(const Job& j) {
@@ -1472,6 +1444,7 @@ int run_job(const Job& j, hipStream_t stream) {
       p.pooling = j.pooling;
       p.idx32 = j.idx32;
       p.off32 = j.off32;
+      p.round_bf16 = j.round_bf16;
       if (v == kVarGeneric) p.sub_threshold = kNoLimit;
       else if (j.sub_threshold == 0) p.sub_threshold = default_sub_threshold(v);
       else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;
@@ -1595,6 +1568,9 @@ int run_all_slots(const void* values, int32_t index_type, const void* val_offset
   j.out = out;
   j.odt = odt;
   j.out_row_stride = static_cast<int64_t>(num_slots) * emb_dim;
+  // the reference's int8 kernel stores acc.to(tl.bfloat16) into an output of the table's dtype
+  // (online_best/infer.py:941, :989-996): fp32 / fp16 outputs get the bf16-rounded value
+  j.round_bf16 = tdt == CTI_EBAG_I8 && odt != CTI_EBAG_BF16;
   return run_job(j, static_cast<hipStream_t>(stream));
 }
 
@@ -1631,16 +1607,14 @@ hipError_t launch_fused_lanes(int lanes, const PoolParams& p, const FusedNorm& f
   }
 }
 
-#ifndef CTI_EBAG_FUSED_SAMPLES
-#define CTI_EBAG_FUSED_SAMPLES 2
-#endif
+constexpr int kFusedSamples = 2;  // measured: 1 / 2 / 4 samples per workgroup 45.7 / 40.5 / 44.6 us
 
-// Samples per fused workgroup: up to CTI_EBAG_FUSED_SAMPLES, while every wavefront's bags fit
+// Samples per fused workgroup: up to kFusedSamples, while every wavefront's bags fit
 // its lanes' bookkeeping and the LDS rows stay within kFusedLdsMax.
 constexpr int64_t kFusedLdsMax = 64 * 1024;
 int fused_samples(int num_slots, int64_t row_out_bytes) {
   const int per_wave = (num_slots + kFusedWaves - 1) / kFusedWaves;
-  int spw = CTI_EBAG_FUSED_SAMPLES;
+  int spw = kFusedSamples;
   while (spw > 1 && (spw * per_wave > kFusedBagsPerWave || spw * row_out_bytes > kFusedLdsMax / 2)) spw /= 2;
   return spw;
 }
@@ -1705,7 +1679,7 @@ extern "C" int cti_ebag_fused_all_slots_layernorm(const void* values, int32_t in
   p.batch = batch_size;
   p.pooling = pooling;
   p.num_fields = num_slots;
-  p.sub_threshold = CTI_EBAG_SUB_THRESHOLD;
+  p.sub_threshold = kSubThreshold;
   p.block_threshold = kNoLimit;
   p.split_threshold = kNoLimit;
   const int64_t rows = max_idx + 1;

@@ -132,7 +132,8 @@ def pack_slots(slots: Sequence[Tuple[torch.Tensor, torch.Tensor]], with_global_o
     return out
 
 
-def merge_batches(batches: Sequence[dict], slot_num: int = 28, with_global_offsets: bool = False) -> dict:
+def merge_batches(batches: Sequence[dict], slot_num: int = 28, with_global_offsets: bool = False,
+                  int32_round_trip: bool = False) -> dict:
     """Concatenate flat-layout sub-batches slot by slot on the GPU.
 
     Same result as _timed_lazy_merge_group_cpu (online_best/infer.py:581-631): for each slot,
@@ -140,6 +141,10 @@ def merge_batches(batches: Sequence[dict], slot_num: int = 28, with_global_offse
     value count, closed by the slot total. Each batch needs ``_flat_values``,
     ``_flat_row_offsets`` and ``_val_offsets`` on one GPU; its batch size is read from the
     offsets length.
+
+    ``int32_round_trip`` gives the pair merge's result instead (_timed_merge_batch_pair,
+    online_best/infer.py:2977-3037): merged values and row offsets pass through int32 (``.int()``
+    then ``.long()``, :3008-3009 and :3019-3020), so values or slot offsets of 2^31 or more wrap.
     """
     if not batches:
         raise ValueError("no batches to merge")
@@ -167,7 +172,8 @@ def merge_batches(batches: Sequence[dict], slot_num: int = 28, with_global_offse
     goff = torch.empty(slot_num * B + 1, dtype=torch.int64, device=dev) if with_global_offsets else None
     lib = _capi.lib()
     with torch.cuda.device(dev):
-        _capi.check(lib.cti_ebag_merge_batches(
+        fn = lib.cti_ebag_merge_batches_int32 if int32_round_trip else lib.cti_ebag_merge_batches
+        _capi.check(fn(
             _ptr_array(vals), _ptr_array(vos), _ptr_array(ros), _i64_array(bs), _i64_array(nnz),
             len(batches), slot_num, flat_values.data_ptr() if total else None, flat_row_offsets.data_ptr(),
             val_offsets.data_ptr(), goff.data_ptr() if goff is not None else None,

@@ -153,8 +153,9 @@ def fused_all_slots_embedding_int8(
 
     ``weight_int8`` int8 [V, emb_dim] and ``scale`` float32 [V] as made by
     ``quantize_embedding_int8``; each bag accumulates ``fma(q, scale[row], acc)`` in fp32 in
-    element order; ``out`` [B, S*emb_dim] is written in its own dtype (fp32 / bf16 / fp16; the
-    reference stores bf16, :940). Returns ``out``.
+    element order; the sum is rounded to bf16, as the reference kernel stores ``acc.to(bfloat16)``
+    (:941), and written into ``out`` [B, S*emb_dim] in out's dtype (fp32 / bf16 / fp16; the
+    reference's ``out`` has the table's dtype, :989). Returns ``out``.
     """
     dev = weight_int8.device
     _require_device_tensor("weight_int8", weight_int8)

@@ -141,6 +141,18 @@ class InputStager:
         self._in_use[slot] = False
 
 
+def _to_device(x, device):
+    """``x`` with every tensor inside it (through dicts, lists and tuples) moved to ``device``
+    with ``non_blocking=True``; anything else is returned as it is."""
+    if isinstance(x, torch.Tensor):
+        return x.to(device, non_blocking=True)
+    if isinstance(x, dict):
+        return {k: _to_device(v, device) for k, v in x.items()}
+    if isinstance(x, (list, tuple)):
+        return type(x)(_to_device(v, device) for v in x)
+    return x
+
+
 def move_model_inputs_to_device(batch: dict, device, slot_num: int = 28,
                                 stager: Optional[InputStager] = None) -> dict:
     """online_best/infer.py:742-779 for the embedding inputs.
@@ -150,8 +162,8 @@ def move_model_inputs_to_device(batch: dict, device, slot_num: int = 28,
     non_blocking=True)`` as in the reference (val_offsets widened to int64, :747). Batches that
     carry only the per-slot pairs ``{i+1: (values, offsets)}`` are moved slot by slot and packed
     on the device by one kernel (``pack_slots``) instead of two ``torch.cat`` and a host tensor
-    (:750-762). ``user_offsets`` and ``_attn_groups`` (inputs of the attention stage) are moved
-    as the reference moves them.
+    (:750-762). Every other string key of the batch (the later stages' inputs, which this path
+    does not read) is passed through with its tensors moved to the device.
     """
     device = torch.device(device)
     if "_flat_values" in batch:
@@ -169,17 +181,7 @@ def move_model_inputs_to_device(batch: dict, device, slot_num: int = 28,
             vals, offs = batch[s]
             slots.append((vals.to(device, non_blocking=True).long(), offs.to(device, non_blocking=True).long()))
         model_batch = dict(pack_slots(slots))
-    if "user_offsets" in batch and "_attn_groups" not in batch:
-        model_batch["user_offsets"] = batch["user_offsets"].to(device, non_blocking=True)
-    if "_attn_groups" in batch:
-        groups = []
-        for g in batch["_attn_groups"]:
-            m = {"rows": g["rows"].to(device, non_blocking=True), "cols": g["cols"].to(device, non_blocking=True),
-                 "num_users": g["num_users"], "max_len": g["max_len"]}
-            if "flat_idx" in g:
-                m["flat_idx"] = g["flat_idx"].to(device, non_blocking=True)
-            if g.get("identity", False):
-                m["identity"] = True
-            groups.append(m)
-        model_batch["_attn_groups"] = groups
+    for key, value in batch.items():
+        if isinstance(key, str) and key not in model_batch and key not in _PARTS:
+            model_batch[key] = _to_device(value, device)
     return model_batch

@@ -217,13 +217,30 @@ int cti_ebag_merge_batches(const int64_t* const* sub_values,
                            int64_t* global_offsets, void* stream);
 
 /*
+ * The pair merge's form of cti_ebag_merge_batches (online_best/infer.py:2977-3037, called in the
+ * timed loop at :3153): the same merge, but the merged values and row offsets pass through int32
+ * as the reference's `.int()` / `.long()` casts take them (:3008-3009, :3019-3020), so an id or a
+ * slot-local offset of 2^31 or more wraps to its low 32 bits read as int32 there and only there.
+ * val_offsets are not cast (:3021); global_offsets[s*B+b] = val_offsets[s] + the wrapped offset.
+ * Arguments as for cti_ebag_merge_batches.
+ */
+int cti_ebag_merge_batches_int32(const int64_t* const* sub_values,
+                                 const int64_t* const* sub_val_offsets,
+                                 const int64_t* const* sub_row_offsets, const int64_t* sub_batch,
+                                 const int64_t* sub_nnz, int32_t num_sub, int32_t num_slots,
+                                 int64_t* flat_values, int64_t* flat_row_offsets, int64_t* val_offsets,
+                                 int64_t* global_offsets, void* stream);
+
+/*
  * int8 variant of the reference-layout entry point, a drop-in for the launch
  *   fused_all_slots_embedding_kernel_int8[(batch_size, num_slots)](values, val_offsets,
  *       row_offsets, weight_int8, scale, out, batch_size, emb_dim, max_idx, BLOCK_SIZE)
  * (online_best/infer.py:904-942, launched at :991-996): as cti_ebag_fused_all_slots, with
  *   weight_int8  int8 [max_idx+1, emb_dim]  and  scale  fp32 [max_idx+1];
- *   acc = fma(q, scale[row], acc) per element in element order, out written in `out_dtype`
- *   (the reference writes bf16, :940).
+ *   acc = fma(q, scale[row], acc) per element in element order. The reference kernel stores
+ *   acc.to(tl.bfloat16) into an output of the table's dtype (:941, :989-996), so the sum is
+ *   rounded to bf16 (nearest even) first and then written in `out_dtype` (fp32: exact widening;
+ *   fp16: rounded again), as the reference's output holds it.
  */
 int cti_ebag_fused_all_slots_int8(const int64_t* values, const int64_t* val_offsets,
                                   const int64_t* row_offsets, const int8_t* weight_int8,
@@ -236,7 +253,8 @@ int cti_ebag_fused_all_slots_int8(const int64_t* values, const int64_t* val_offs
  * (or its int8 form) with
  *   values       [nnz] of `index_type` (CTI_EBAG_I64 / CTI_EBAG_I32)
  *   val_offsets  [num_slots], row_offsets [num_slots*(B+1)], both of `offset_type` (I64 / I32)
- *   table_dtype  F32 / BF16 / F16, or I8 with `scale` fp32 [max_idx+1] (else ignored)
+ *   table_dtype  F32 / BF16 / F16, or I8 with `scale` fp32 [max_idx+1] (else ignored; I8 results
+ *                are rounded to bf16 before `out_dtype`, as in cti_ebag_fused_all_slots_int8)
  *   out          [B, num_slots*emb_dim] of `out_dtype`
  * The Triton kernel specialises on the dtypes of its pointer arguments, so the reference launch
  * (online_best/infer.py:1052-1059) accepts int32 inputs the same way; the int32 forms halve the

@@ -23,12 +23,28 @@ def bench():
 def test_profiles_give_the_traffic(bench, workload, kernel):
     # every profile the bench line cites exists and carries its measured HBM bytes per launch,
     # which sit between the output bytes written and 4 GB
-    t = bench.traffic_from_profiles(workload, kernel)
+    t, source = bench.traffic_from_profiles(workload, kernel)
     assert t is not None and 2.9e7 < t < 4e9
+    assert source == f"profiles/{kernel}_{workload}.md" and os.path.exists(os.path.join(ROOT, source))
 
 
 def test_missing_profile_gives_null_traffic(bench):
-    assert bench.traffic_from_profiles("no-such-workload") is None
+    assert bench.traffic_from_profiles("no-such-workload") == (None, None)
+
+
+def test_roofline_reports_the_dram_fraction(bench):
+    r = bench.roofline(6000.0, 240e6, 40e-6, "pool_kernel", ("bf16-2m", "pool_kernel"))
+    assert r["frac"] == pytest.approx(0.75)
+    assert r["dram_frac"] == pytest.approx(r["traffic"] / 40e-6 / 1e9 / 8000.0)
+    assert r["traffic_source"] == "profiles/pool_kernel_bf16-2m.md"
+    assert bench.roofline(1.0, 1.0, 1.0, "k", None)["dram_frac"] is None
+
+
+def test_host_cpu_counts(bench):
+    info = bench.host_cpus()
+    assert info["logical"] == os.cpu_count()
+    assert 1 <= info["affinity"] <= info["logical"]
+    assert info["physical"] is None or 1 <= info["physical"] <= info["logical"]
 
 
 def test_more_than_one_gpu_is_refused():

@@ -150,6 +150,10 @@ def test_pack_and_merge_reject_bad_arguments(pkg):
     assert lib.cti_ebag_merge_batches(many, many, many, bs, bs, 2, 40000, 16, 16, 16, None, None) == c.EUNSUPPORTED
     neg = (ctypes.c_int64 * 2)(-1, 1)
     assert lib.cti_ebag_merge_batches(many, many, many, neg, bs, 2, 28, 16, 16, 16, None, None) == c.EINVAL
+    # the pair merge's int32 form checks its arguments the same way
+    assert lib.cti_ebag_merge_batches_int32(many, many, many, bs, bs, 33, 28, 16, 16, 16, None, None) == c.EUNSUPPORTED
+    assert lib.cti_ebag_merge_batches_int32(many, many, many, neg, bs, 2, 28, 16, 16, 16, None, None) == c.EINVAL
+    assert lib.cti_ebag_merge_batches_int32(many, many, many, bs, bs, 0, 28, None, None, None, None, None) == c.OK
 
 
 def test_workspace_query(pkg):

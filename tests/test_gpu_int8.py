@@ -185,6 +185,36 @@ def test_int8_fused_all_slots_reference_layout(pkg, dev):
     assert np.array_equal(to_np(out, "bf16"), want)
 
 
+@pytest.mark.parametrize("odt", ["f32", "f16"])
+@pytest.mark.parametrize("idx", [torch.int64, torch.int32])
+def test_int8_reference_layout_rounds_through_bf16(pkg, dev, odt, idx):
+    """The reference's int8 kernel stores acc.to(tl.bfloat16) into an output of the table's dtype
+    (online_best/infer.py:941, :989-996): with an fp32 / fp16 output the drop-in must hold the
+    bf16-rounded sum, widened (fp32) or converted again (fp16)."""
+    rng = np.random.default_rng(41)
+    S, B, V, D = 28, 65, 3000, 128
+    q = rng.integers(-128, 128, (V, D)).astype(np.int8)
+    sc = (rng.random(V) * 0.01 + 1e-5).astype(np.float32)
+    L = rng.integers(0, 12, (S, B))
+    ro = np.zeros((S, B + 1), np.int64)
+    np.cumsum(L, axis=1, out=ro[:, 1:])
+    vo = np.concatenate([[0], np.cumsum(L.sum(axis=1))[:-1]]).astype(np.int64)
+    values = rng.integers(-3, V + 3, int(L.sum())).astype(np.int64)
+    bf = orc.decode(orc.pool_c(values, ro.reshape(-1), [(q, sc)] * S, "i8", "sum", "bf16", batch=B, val_base=vo),
+                    "bf16")
+    single = orc.pool_c(values, ro.reshape(-1), [(q, sc)] * S, "i8", "sum", "f32", batch=B, val_base=vo)
+    want = bf.astype(np.float32) if odt == "f32" else bf.astype(np.float16)
+    assert not np.array_equal(single, bf)  # the bf16 rounding is visible
+    out = torch.empty((B, S * D), dtype=TORCH_DT[odt], device=dev)
+    pkg.fused_all_slots_embedding_int8(torch.from_numpy(values).to(dev, idx), torch.from_numpy(vo).to(dev),
+                                       torch.from_numpy(ro.reshape(-1)).to(dev), torch.from_numpy(q).to(dev),
+                                       torch.from_numpy(sc).to(dev), out, B, D, V - 1)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32 if odt == "f32" else np.uint16),
+                          want.view(np.uint32 if odt == "f32" else np.uint16))
+
+
 def test_int8_matches_dequantised_float_tables_within_rounding(pkg, dev):
     """Quantise a bf16 table on the device, pool both; the int8 result tracks the bf16 one within
     the quantisation error (half a step per element, summed over the bag)."""

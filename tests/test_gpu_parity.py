@@ -408,6 +408,42 @@ def test_merge_batches_matches_restatement_and_pooling_commutes(pkg, dev):
     assert torch.equal(merged, torch.cat(parts, dim=0))
 
 
+def test_pair_merge_int32_round_trip(pkg, dev):
+    """merge_batches(int32_round_trip=True) is the pair merge (online_best/infer.py:2977-3037): the
+    merged values pass through int32, so ids of 2^31 or more wrap there (and nowhere else), and the
+    pooled result is the pooling of the wrapped ids. Slot offsets of 2^31 or more would wrap the
+    same way; they need batches of 2^31 ids, so only the values' wrap is exercised here."""
+    S = 28
+    subs = [random_case(90 + k, F=S, B=B, dims=(128,), V=(2000,), tdt="bf16") for k, B in enumerate((33, 5, 60))]
+    rng = np.random.default_rng(5)
+    lays, dev_batches = [], []
+    for c in subs:
+        m = rng.random(c.values.size) < 0.1
+        c.values[m] = rng.integers(2 ** 31, 2 ** 33, int(m.sum())) * rng.choice([-1, 1], int(m.sum()))
+        ro, vo = c.reference_layout()
+        lays.append((c.values, ro, vo))
+        dev_batches.append({"_flat_values": torch.from_numpy(c.values).to(dev),
+                            "_flat_row_offsets": torch.from_numpy(ro).to(dev),
+                            "_val_offsets": torch.from_numpy(vo).to(dev)})
+    v, ro, vo = orc.merge_pair_layouts(lays, S)
+    v_lazy, _, _ = orc.merge_layouts(lays, S)
+    assert not np.array_equal(v, v_lazy)  # the wrap is visible in this batch
+    got = pkg.merge_batches(dev_batches, S, with_global_offsets=True, int32_round_trip=True)
+    plain = pkg.merge_batches(dev_batches, S)
+    torch.cuda.synchronize()
+    assert np.array_equal(got["_flat_values"].cpu().numpy(), v)
+    assert np.array_equal(got["_flat_row_offsets"].cpu().numpy(), ro)
+    assert np.array_equal(got["_val_offsets"].cpu().numpy(), vo)
+    assert np.array_equal(plain["_flat_values"].cpu().numpy(), v_lazy)
+    B = sum(c.B for c in subs)
+    assert np.array_equal(got["offsets"].cpu().numpy(), orc.to_global_offsets(vo, ro, B, len(v)))
+    w = to_dev(subs[0].tables[0], "bf16", dev)
+    pooled = pkg.fused_embedding(got, w, S)
+    torch.cuda.synchronize()
+    want = orc.pool_c(v, ro, [subs[0].tables[0]] * S, "bf16", "sum", batch=B, val_base=vo)
+    assert np.array_equal(to_np(pooled, "bf16"), want)
+
+
 # ---- configuration-sized workloads -------------------------------------------------------------
 def _sampled_check(pkg, wl, tables, out, rng, n_sample=400, bag_filter=None):
     """Compare sampled bags (plus every empty, clamped-free longest bag per field) with the oracle
@@ -498,5 +534,61 @@ def test_lazy_grouped_workload(pkg, dev):
         parts.append(pkg.embedding_bag_pooled(v, o, tables, pooling="mean", out_dtype=torch.bfloat16))
     assert torch.equal(out.view(torch.int16), torch.cat(parts, dim=0).view(torch.int16))
     _sampled_check(pkg, wl, tables, out, np.random.default_rng(1))
+    del tables
+    torch.cuda.empty_cache()
+
+
+# The binned path hetero-bf16 is measured with: binning pass, mixed-width main kernel, list kernel
+# with bags of 33..192 rows on one wavefront each and longer bags split over a workgroup.
+HETERO_BINS = dict(use_bins=True, block_threshold=32, split_threshold=192)
+
+
+def test_hetero_binned_full_size(pkg, dev):
+    """hetero-bf16 at full size (B = 8192) through the binned launch sequence its timings come
+    from: sampled bags (more of them, so the split list is hit) against the oracle, short bags bit
+    for bit, and the same output as the unbinned launch within the reassociation bound."""
+    W = pkg.workloads
+    wl = W.make("hetero-bf16", seed=0)
+    L = wl.lengths().reshape(wl.num_fields, wl.batch)
+    print(f"[hetero-bf16 binned] B={wl.batch} nnz={wl.nnz} bags>192: {(L > 192).sum()} bags 33..192: "
+          f"{((L > 32) & (L <= 192)).sum()}", flush=True)
+    assert (L > 192).sum() > 1000 and ((L > 32) & (L <= 192)).sum() > 1000
+    tables = W.make_tables(wl, dev, seed=0)
+    v, o = W.to_device(wl, dev)
+    out = pkg.embedding_bag_pooled(v, o, tables, pooling=wl.pooling, out_dtype=wl.out_dtype, **HETERO_BINS)
+    torch.cuda.synchronize()
+    _sampled_check(pkg, wl, tables, out, np.random.default_rng(7), n_sample=4000)
+    out2 = pkg.embedding_bag_pooled(v, o, tables, pooling=wl.pooling, out_dtype=wl.out_dtype, **HETERO_BINS)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))  # deterministic
+    del tables
+    torch.cuda.empty_cache()
+
+
+def test_hetero_binned_full_size_integer_tables_bitwise(pkg, dev):
+    """The same binned launch on integer-valued bf16 tables in [-32, 32]: every partial sum is
+    exact in fp32 (|sum| <= 2048 * 32 < 2^24), so each output is the bf16 rounding of the exact
+    sum whatever the order, and the whole [8192, 2048] output must equal the oracle bit for bit
+    (index, offset, segment and list handling of every bag)."""
+    W = pkg.workloads
+    wl = W.make("hetero-bf16", seed=0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    tables = [torch.randint(-32, 33, (wl.vocab[f], wl.dims[f]), generator=g, device=dev).to(torch.bfloat16)
+              for f in range(wl.num_fields)]
+    v, o = W.to_device(wl, dev)
+    out = pkg.embedding_bag_pooled(v, o, tables, pooling=wl.pooling, out_dtype=torch.bfloat16, **HETERO_BINS)
+    torch.cuda.synchronize()
+    got = to_np(out, "bf16")
+    B = wl.batch
+    col = 0
+    for f in range(wl.num_fields):
+        s, e = int(wl.offsets[f * B]), int(wl.offsets[(f + 1) * B])
+        ids = np.clip(wl.values[s:e], 0, wl.vocab[f] - 1)
+        uniq, inv = np.unique(ids, return_inverse=True)
+        rows = tables[f].index_select(0, torch.from_numpy(uniq).to(dev)).cpu().view(torch.int16).numpy().view(np.uint16)
+        offs = (wl.offsets[f * B:(f + 1) * B + 1] - s).astype(np.int64)
+        want = orc.pool_c(inv.astype(np.int64), offs, [rows], "bf16", "sum", "bf16")
+        assert np.array_equal(got[:, col:col + wl.dims[f]], want), f"field {f} (D={wl.dims[f]})"
+        col += wl.dims[f]
     del tables
     torch.cuda.empty_cache()

@@ -1,12 +1,15 @@
 """int32 inputs and the host -> device staging path on the GPU.
 
 Bar: the pooled output from int32 ids / offsets, and from batches moved by InputStager (pinned,
-int32-compacted, double-buffered), is bit-identical to the int64 path's, including ids outside
-the int32 range (saturated on the host, clamped on the device).
+int32-compacted, double-buffered), equals the oracle's pooling of the host batch bit for bit
+(bags of at most 12 rows: one lane group each, element order), including ids outside the int32
+range (saturated on the host, clamped on the device), and equals the int64 path's.
 """
 import numpy as np
 import pytest
 import torch
+
+from oracle import ebag_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -26,16 +29,27 @@ def host_batch(rng, B, max_len=12, wide_ids=True):
             "_val_offsets": torch.from_numpy(vo)}, B
 
 
+def oracle_pool(hb, weight, B):
+    """The oracle's pooling of a host batch (int64 ids as the collate leaves them) as bf16 bits."""
+    wbits = weight.cpu().view(torch.int16).numpy().view(np.uint16)
+    return orc.pool_c(hb["_flat_values"].numpy(), hb["_flat_row_offsets"].numpy(), [wbits] * S, "bf16", "sum",
+                      batch=B, val_base=hb["_val_offsets"].numpy())
+
+
 def pool(pkg, dev_batch, weight, B):
     out = torch.empty((B, S * D), dtype=weight.dtype, device=weight.device)
     return pkg.fused_all_slots_embedding(dev_batch["_flat_values"], dev_batch["_val_offsets"],
                                          dev_batch["_flat_row_offsets"], weight, out, B, D, V - 1)
 
 
-@pytest.fixture(scope="module")
-def weight(dev):
+def weight_of(dev):
     g = torch.Generator(device="cpu").manual_seed(1)
     return torch.randn(V, D, generator=g).to(torch.bfloat16).to(dev)
+
+
+@pytest.fixture(scope="module")
+def weight(dev):
+    return weight_of(dev)
 
 
 @pytest.mark.parametrize("vt,ot", [(torch.int32, torch.int32), (torch.int32, torch.int64), (torch.int64, torch.int32)])
@@ -48,6 +62,7 @@ def test_int32_layouts_match_int64(pkg, dev, weight, vt, ot):
     got = pool(pkg, narrow, weight, B)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    assert np.array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16), oracle_pool(hb, weight, B))
 
 
 def test_int32_mixed_offset_types_and_int8(pkg, dev, weight):
@@ -81,6 +96,7 @@ def test_stager_pipeline_matches_direct_transfer(pkg, dev, weight, compact, dept
         stager.release(staged)
     torch.cuda.synchronize()
     for (hb, B), g in zip(batches, got):
+        assert np.array_equal(g.cpu().view(torch.int16).numpy().view(np.uint16), oracle_pool(hb, weight, B))
         ref = pool(pkg, pkg.move_model_inputs_to_device(hb, dev, S), weight, B)
         torch.cuda.synchronize()
         assert torch.equal(g.view(torch.int16), ref.view(torch.int16))
@@ -119,3 +135,23 @@ def test_per_slot_pairs_are_packed_on_device(pkg, dev, weight):
     moved = pkg.move_model_inputs_to_device(pairs, dev, S)
     for k in ("_flat_values", "_flat_row_offsets", "_val_offsets"):
         assert torch.equal(moved[k].cpu(), hb[k])
+
+
+def test_other_batch_keys_pass_through(pkg, dev):
+    """Keys the pooling step does not read are passed on, their tensors moved to the device
+    (nested lists / dicts too) and everything else unchanged."""
+    rng = np.random.default_rng(12)
+    hb, B = host_batch(rng, 9, wide_ids=False)
+    hb = dict(hb)
+    hb["user_offsets"] = torch.arange(4)
+    hb["_attn_groups"] = [{"rows": torch.arange(3), "num_users": 2, "identity": True}]
+    for stager in (None, pkg.InputStager(hb["_flat_values"].numel(), S, B, dev)):
+        moved = pkg.move_model_inputs_to_device(hb, dev, S, stager=stager)
+        assert moved["user_offsets"].device.type == "cuda" and torch.equal(moved["user_offsets"].cpu(), torch.arange(4))
+        grp = moved["_attn_groups"][0]
+        assert grp["rows"].device.type == "cuda" and grp["num_users"] == 2 and grp["identity"] is True
+        got = pool(pkg, moved, weight_of(dev), B)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16), oracle_pool(hb, weight_of(dev), B))
+        if stager is not None:
+            stager.release(moved)
