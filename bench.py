@@ -62,6 +62,8 @@ WORKLOAD_TEXT = {
                    "20 Poisson(2) + 8 lognormal(median 64, max 2048) fields, sum",
     "lazy-32k": "28 fields, bf16 tables 4,000,000 x 128, B=32768 from 8 merged sub-batches, Zipf(0.8), mean",
     "small-fp32": "28 fields, fp32 tables 10,000 x 64, B=256, Poisson(3) lengths, sum",
+    "reference-5m": "28 slots over one shared bf16 table 5,000,000 x 512 (the reference's nn.Embedding), B=4096, "
+                    "geometric(mean 8) lengths, Zipf(1.1) ids, sum, bf16 output [4096, 28*512]",
 }
 # Workloads whose launches end faster when tiles start longest-first (the order is made one step
 # ahead inside the previous launch). lazy-32k is slower with it (its launch is DRAM-bound and the
@@ -212,7 +214,7 @@ def bench_h2d(args, pkg, wls, dev):
 
     def pool(db):
         pkg.fused_all_slots_embedding(db["_flat_values"], db["_val_offsets"], db["_flat_row_offsets"], weight, out,
-                                      B, D, V - 1)
+                                      B, D, V - 1, tile_order=db.get("_tile_order"))
 
     def run(step, K, W):
         for i in range(W):
@@ -240,9 +242,12 @@ def bench_h2d(args, pkg, wls, dev):
             pkg._capi.check(pkg._capi.lib().cti_ebag_narrow_ids(t.data_ptr(), t.numel(), d.data_ptr(), 16))
             h32[k] = d
         host32.append(h32)
-    for name, compact, src in (("pinned_int64_overlapped", False, host), ("pinned_int32_overlapped", True, host),
-                               ("pinned_int32_from_int32_overlapped", True, host32)):
-        stager = pkg.InputStager(max_nnz, F, B, dev, depth=2, compact=compact)
+    for name, compact, src, order in (("pinned_int64_overlapped", False, host, False),
+                                      ("pinned_int32_overlapped", True, host, False),
+                                      ("pinned_int32_from_int32_overlapped", True, host32, False),
+                                      ("pinned_int32_ordered_overlapped", True, host, True)):
+        stager = pkg.InputStager(max_nnz, F, B, dev, depth=2, compact=compact,
+                                 order_for=(wl0.table_dtype, D) if order else None)
 
         def staged(i, stager=stager, src=src):
             db = pkg.move_model_inputs_to_device(src[i % n], dev, F, stager=stager)
@@ -266,11 +271,15 @@ def bench_h2d(args, pkg, wls, dev):
         del hbuf, dbuf
     resident = [pkg.move_model_inputs_to_device(h, dev, F) for h in host]
     results["pool_only_resident_int64"] = run(lambda i: pool(resident[i % n]), args.steps, args.warmup)
+    # the same resident batches, each with the order its collate would make on the host
+    for h, r in zip(host, resident):
+        r["_tile_order"] = pkg.make_tile_order(h["_flat_row_offsets"], B, F, wl0.table_dtype, D).to(dev)
+    results["pool_only_resident_int64_ordered"] = run(lambda i: pool(resident[i % n]), args.steps, args.warmup)
     bags = wl0.num_bags
     nnz_mean = float(np.mean([h["_flat_values"].numel() for h in host]))
     bytes64 = 8 * (nnz_mean + F * (B + 1) + F)
     best = min(("reference_pageable_int64", "pinned_int64_overlapped", "pinned_int32_overlapped",
-                "pinned_int32_from_int32_overlapped"), key=lambda k: results[k])
+                "pinned_int32_from_int32_overlapped", "pinned_int32_ordered_overlapped"), key=lambda k: results[k])
     rec = {
         "metric": "end-to-end pooled bags/sec from host flat-layout batches (H2D + pooling), B=4096x28 fields, D=128 bf16",
         "value": bags / results[best],
@@ -316,9 +325,20 @@ def bench_encoder(args, pkg, wls, dev):
     out = torch.empty((B, F * D), dtype=wl0.table_dtype, device=dev)
     n = len(batches)
 
-    def separate(i):
+    # each batch's dispatch order, as its collate would make it on the host from the offsets
+    orders = [pkg.make_tile_order(ro.cpu(), B, F, wl0.table_dtype, D).to(dev) for _, _, ro in batches]
+
+    def pool_plain(i):
         v, vo, ro = batches[i % n]
         pkg.fused_all_slots_embedding(v, vo, ro, weight, out, B, D, V - 1)
+
+    def pool_ordered(i):
+        v, vo, ro = batches[i % n]
+        pkg.fused_all_slots_embedding(v, vo, ro, weight, out, B, D, V - 1, tile_order=orders[i % n])
+
+    def separate(i):
+        v, vo, ro = batches[i % n]
+        pkg.fused_all_slots_embedding(v, vo, ro, weight, out, B, D, V - 1, tile_order=orders[i % n])
         pkg.layer_norm(out, gamma, beta, 1e-5, out=out)
 
     def fused(i):
@@ -337,6 +357,9 @@ def bench_encoder(args, pkg, wls, dev):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / args.steps / 1e3
 
+    log("drop-in pooling, plain and with host-made orders")
+    t_plain = timed(pool_plain)
+    t_ordered = timed(pool_ordered)
     log("pooling then LayerNorm")
     t_sep = timed(separate)
     log("fused")
@@ -361,9 +384,127 @@ def bench_encoder(args, pkg, wls, dev):
                 "gamma ~ N(1, 0.1), beta ~ N(0, 0.1)",
         "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}; reference layout, one shared "
                                "table, sum pooling, then LayerNorm over [B, 28*128]"},
-        "us_per_step": {"pool_then_layernorm": t_sep * 1e6, "fused": t_fused * 1e6},
+        "us_per_step": {"pool_then_layernorm": t_sep * 1e6, "fused": t_fused * 1e6,
+                        "pool_drop_in": t_plain * 1e6, "pool_drop_in_host_order": t_ordered * 1e6},
         "roofline": roofline(achieved, fused_bytes, t_fused, "pool_norm_kernel",
                              (args.workload + "-shared", "pool_norm_kernel")),
+        "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def reference_layout(wl, dev):
+    """(values, val_offsets, row_offsets) of a workload in the reference's flat layout, on dev."""
+    import numpy as np
+    import torch
+
+    F, B = wl.num_fields, wl.batch
+    off = wl.offsets
+    ro = np.stack([off[f * B:(f + 1) * B + 1] - off[f * B] for f in range(F)]).reshape(-1)
+    return (torch.from_numpy(wl.values).to(dev), torch.from_numpy(off[0:F * B:B].copy()).to(dev),
+            torch.from_numpy(ro).to(dev))
+
+
+def bench_reference(args, pkg, dev):
+    """The reference's own shape: 28 slots over one shared bf16 [5,000,000, 512] table (5.12 GB,
+    so rows past 4 GiB are addressed with 64-bit offsets), reference layout, sum: the drop-in
+    pooling launch, pooling with the input LayerNorm over 14,336 columns fused, and the int8
+    table. A second leg compares the two addressing paths on identical batches: ids below
+    4,194,303 pooled from the 5M-row table (64-bit addresses) and from a 4,194,303-row table
+    (which fits the 32-bit buffer path)."""
+    import numpy as np
+    import torch
+
+    W = pkg.workloads
+    V, D, F = 5_000_000, 512, 28
+    log(f"reference-5m: generating {args.sets} index sets")
+    wls = [W.make("reference-5m", seed=s) for s in range(1, args.sets + 1)]
+    B = wls[0].batch
+    batches = [reference_layout(wl, dev) for wl in wls]
+    log("filling the shared [5,000,000, 512] bf16 table")
+    weight = W.make_tables(wls[0], dev, seed=0)[0]
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    gamma = torch.empty(F * D, dtype=torch.bfloat16, device=dev).normal_(1.0, 0.1, generator=g)
+    beta = torch.empty(F * D, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.1, generator=g)
+    out = torch.empty((B, F * D), dtype=torch.bfloat16, device=dev)
+    n = len(batches)
+
+    def timed(step):
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            step(args.warmup + i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps / 1e3
+
+    def pool(i, w=weight, bs=batches):
+        v, vo, ro = bs[i % len(bs)]
+        pkg.fused_all_slots_embedding(v, vo, ro, w, out, B, D, w.shape[0] - 1)
+
+    def fused(i):
+        v, vo, ro = batches[i % n]
+        pkg.fused_all_slots_embedding_layernorm(v, vo, ro, weight, out, B, D, V - 1, gamma, beta, 1e-5)
+
+    us = {}
+    log("drop-in pooling")
+    us["pool"] = timed(pool) * 1e6
+    log("pooling + LayerNorm fused")
+    us["pool_layernorm_fused"] = timed(fused) * 1e6
+
+    def pool_int8(i):
+        v, vo, ro = batches[i % n]
+        pkg.fused_all_slots_embedding_int8(v, vo, ro, q, sc, out, B, D, V - 1)
+
+    log("quantising the table to int8")
+    q, sc = pkg.quantize_embedding_int8(weight)
+    log("int8 pooling")
+    us["pool_int8"] = timed(pool_int8) * 1e6
+    del q, sc
+    torch.cuda.empty_cache()
+
+    # the addressing paths on identical batches: ids < 4,194,303 (so no clamp differs)
+    V4 = (1 << 32) // (D * 2) - 1
+    log("addressing paths: index sets over 4,194,303 rows")
+    wl4 = [W.make("reference-5m", seed=s, vocab=V4) for s in range(1, args.sets + 1)]
+    b4 = [reference_layout(wl, dev) for wl in wl4]
+    us["pool_64bit_addresses_ids_below_4gib"] = timed(lambda i: pool(i, weight, b4)) * 1e6
+    del weight
+    torch.cuda.empty_cache()
+    w4 = torch.empty((V4, D), dtype=torch.bfloat16, device=dev).normal_(0.0, 0.01, generator=g)
+    us["pool_buffer_path_table_below_4gib"] = timed(lambda i: pool(i, w4, b4)) * 1e6
+
+    def alg_bytes(wl, tb=2, extra=0):
+        # each lookup's row, ids, the reference layout's offsets, the output
+        return wl.nnz * (D * tb + extra) + wl.nnz * 8 + (F * (B + 1) + F) * 8 + B * F * D * 2
+
+    pool_bytes = float(np.mean([alg_bytes(wl) for wl in wls]))
+    int8_bytes = float(np.mean([alg_bytes(wl, 1, 4) for wl in wls]))
+    b4_bytes = float(np.mean([alg_bytes(wl) for wl in wl4]))
+    fused_bytes = pool_bytes + 2 * F * D * 2
+    t = us["pool"] / 1e6
+    rec = {
+        "metric": "pooled bags/sec at the reference's own table shape (one shared bf16 [5e6, 512] table, 28 slots)",
+        "value": B * F / t, "unit": "bags/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": t * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": f"synthetic: {n} seeded index sets rotated, shared N(0, 0.01) table, gamma ~ N(1, 0.1), "
+                "beta ~ N(0, 0.1)",
+        "config": {"workload": f"reference-5m: {WORKLOAD_TEXT['reference-5m']}",
+                   "nnz_mean": float(np.mean([wl.nnz for wl in wls]))},
+        "us_per_step": us,
+        "roofline": roofline(pool_bytes / t / 1e9, pool_bytes, t, "pool_kernel", ("reference-5m", "pool_kernel")),
+        "roofline_fused_layernorm": roofline(fused_bytes / (us["pool_layernorm_fused"] / 1e6) / 1e9, fused_bytes,
+                                             us["pool_layernorm_fused"] / 1e6, "pool_norm_kernel",
+                                             ("reference-5m", "pool_norm_kernel")),
+        "roofline_int8": roofline(int8_bytes / (us["pool_int8"] / 1e6) / 1e9, int8_bytes, us["pool_int8"] / 1e6,
+                                  "pool_kernel", ("reference-5m-int8", "pool_kernel")),
+        "addressing": {"bytes_per_launch": b4_bytes,
+                       "frac_64bit": b4_bytes / (us["pool_64bit_addresses_ids_below_4gib"] / 1e6) / 1e9 / HBM_PEAK_GBS,
+                       "frac_buffer": b4_bytes / (us["pool_buffer_path_table_below_4gib"] / 1e6) / 1e9 / HBM_PEAK_GBS},
         "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
@@ -570,7 +711,7 @@ def main():
     ap.add_argument("--bins", action="store_true", help="run the device length-binning pass")
     ap.add_argument("--block-threshold", type=int, default=0)
     ap.add_argument("--split-threshold", type=int, default=0)
-    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d", "encoder", "layout"],
+    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d", "encoder", "layout", "reference"],
                     help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
                          "step end to end from host batches")
     ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
@@ -614,6 +755,8 @@ def main():
 
     if args.stage == "layout":
         return bench_layout(args, pkg, dev)
+    if args.stage == "reference":
+        return bench_reference(args, pkg, dev)
     log(f"workload {args.workload}: generating {args.sets} index sets")
     wls = [W.make(args.workload, seed=s) for s in range(1, args.sets + 1)]
     wl0 = wls[0]

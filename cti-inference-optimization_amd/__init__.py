@@ -14,6 +14,7 @@ Public surface:
   pack_slots, merge_batches                   GPU builders of the flat layout
   InputStager, move_model_inputs_to_device    pinned, int32-compacted, overlapped transfer of
                                               host batches to the GPU
+  make_tile_order, order_bytes                a batch's dispatch order, made on the host
 """
 from . import workloads
 from ._capi import EbagError, lib as load_library
@@ -21,7 +22,8 @@ from .encoder import RepEncoder
 from .layout import collate_flat_layout, merge_batches, pack_slots, prebuild_flat_layout
 from .staging import InputStager, move_model_inputs_to_device
 from .ops import (PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_all_slots_embedding_int8,
-                  fused_all_slots_embedding_layernorm, fused_embedding, layer_norm, quantize_embedding_int8)
+                  fused_all_slots_embedding_layernorm, fused_embedding, layer_norm, make_tile_order, order_bytes,
+                  quantize_embedding_int8)
 
 __all__ = [
     "EbagError",
@@ -41,5 +43,7 @@ __all__ = [
     "fused_all_slots_embedding_layernorm",
     "quantize_embedding_int8",
     "layer_norm",
+    "make_tile_order",
+    "order_bytes",
     "workloads",
 ]

@@ -1528,7 +1528,8 @@ namespace {
 // type and index / offset width; `scale` is the int8 table's per-row scale.
 int run_all_slots(const void* values, int32_t index_type, const void* val_offsets, const void* row_offsets,
                   int32_t offset_type, const void* weight, const float* scale, int32_t tdt, void* out, int32_t odt,
-                  int64_t batch_size, int32_t num_slots, int32_t emb_dim, int64_t max_idx, int64_t nnz, void* stream) {
+                  int64_t batch_size, int32_t num_slots, int32_t emb_dim, int64_t max_idx, int64_t nnz, void* stream,
+                  const int32_t* tile_order = nullptr, int64_t order_bytes = 0) {
   if (index_type != CTI_EBAG_I64 && index_type != CTI_EBAG_I32)
     return set_error(CTI_EBAG_EINVAL, "unknown index type code %d", index_type);
   if (offset_type != CTI_EBAG_I64 && offset_type != CTI_EBAG_I32)
@@ -1571,6 +1572,8 @@ int run_all_slots(const void* values, int32_t index_type, const void* val_offset
   // the reference's int8 kernel stores acc.to(tl.bfloat16) into an output of the table's dtype
   // (online_best/infer.py:941, :989-996): fp32 / fp16 outputs get the bf16-rounded value
   j.round_bf16 = tdt == CTI_EBAG_I8 && odt != CTI_EBAG_BF16;
+  j.tile_order = tile_order;
+  j.order_bytes = order_bytes;
   return run_job(j, static_cast<hipStream_t>(stream));
 }
 
@@ -1830,4 +1833,120 @@ extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t 
   const int rc = validate_tables(j);
   if (rc != CTI_EBAG_OK) return rc;
   return run_job(j, static_cast<hipStream_t>(stream));
+}
+
+namespace cti {
+namespace {
+
+// Rows per bag of a tile -> its bucket (0 = most rows per bag), as order_next computes it.
+inline int order_bucket(int64_t rows, int nb) {
+  int64_t per_bag = rows >= 0 ? rows >> __builtin_ctz(static_cast<unsigned>(nb)) : 0;  // nb is a power of two
+  per_bag = per_bag < 0 ? 0 : (per_bag > kOrderBuckets - 1 ? kOrderBuckets - 1 : per_bag);
+  return kOrderBuckets - 1 - static_cast<int>(per_bag);
+}
+
+inline int64_t host_offset(const void* a, int32_t type, int64_t i) {
+  return type == CTI_EBAG_I32 ? static_cast<int64_t>(static_cast<const int32_t*>(a)[i])
+                              : static_cast<const int64_t*>(a)[i];
+}
+
+}  // namespace
+}  // namespace cti
+
+extern "C" int cti_ebag_order_host(const void* row_offsets, int32_t offset_type, int64_t batch_size, int32_t num_slots,
+                                   int32_t table_dtype, int32_t emb_dim, int32_t* order, int64_t order_bytes) {
+  clear_error();
+  if (offset_type != CTI_EBAG_I64 && offset_type != CTI_EBAG_I32)
+    return set_error(CTI_EBAG_EINVAL, "unknown offset type code %d", offset_type);
+  if (!dtype_ok(table_dtype) && table_dtype != CTI_EBAG_I8)
+    return set_error(CTI_EBAG_EINVAL, "unknown table dtype code %d", table_dtype);
+  if (batch_size < 1 || num_slots < 1 || emb_dim < 1)
+    return set_error(CTI_EBAG_EINVAL, "batch_size, num_slots and emb_dim must be >= 1");
+  if (!row_offsets || !order) return set_error(CTI_EBAG_EINVAL, "NULL host pointer among row_offsets/order");
+  if (num_slots > kMaxFields)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "a dispatch order covers at most %d slots (got %d)", kMaxFields, num_slots);
+  // the row shape the reference-layout launch takes for aligned buffers
+  cti_ebag_table t;
+  memset(&t, 0, sizeof(t));
+  t.data = reinterpret_cast<const void*>(uintptr_t{256});
+  t.rows = 1;
+  t.row_stride = emb_dim;
+  t.dim = emb_dim;
+  const int variant = pick_variant(t, dtype_bytes(table_dtype), 4, reinterpret_cast<void*>(uintptr_t{256}),
+                                   static_cast<int64_t>(emb_dim) * 4);
+  if (variant == kVarGeneric)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "rows of %d elements of this type take the element-wise kernel, which "
+                     "follows no order", emb_dim);
+  const int nb = bags_per_tile(variant);
+  const int64_t per_field = (batch_size + nb - 1) / nb;
+  const int64_t n = per_field * num_slots;
+  if (n > INT32_MAX / 2) return set_error(CTI_EBAG_EUNSUPPORTED, "batch of %lld samples has too many tiles", (long long)batch_size);
+  if (order_bytes < (kOrderHeader + n) * 4)
+    return set_error(CTI_EBAG_EINVAL, "order buffer of %lld bytes; this batch needs %lld", (long long)order_bytes,
+                     (long long)((kOrderHeader + n) * 4));
+  // Per XCD range (the tiles xcd_contiguous() gives one XCD) and per chunk of kOrderChunk tiles: a
+  // stable counting sort by bucket, as the device's order_next makes it (whose order inside a
+  // bucket is arbitrary).
+  const int64_t q = n >> 3, r = n & 7;
+  std::vector<unsigned char> bucket(kOrderChunk);
+  for (int x = 0; x < 8; ++x) {
+    const int64_t lo = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+    const int64_t cnt = q + (x < r ? 1 : 0);
+    for (int64_t c0 = 0; c0 < cnt; c0 += kOrderChunk) {
+      const int64_t m = cnt - c0 < kOrderChunk ? cnt - c0 : kOrderChunk;
+      // four interleaved counts, so that runs of tiles in one bucket do not form one chain of
+      // dependent increments
+      int32_t cnt4[4][kOrderBuckets] = {};
+      // tiles of a chunk are consecutive: walk (field, tile in field) instead of dividing per tile
+      int64_t fi = (lo + c0) / per_field, local = lo + c0 - fi * per_field;
+      for (int64_t k = 0; k < m; ++k) {
+        const int64_t b0 = local * nb;
+        const int64_t b1 = b0 + nb < batch_size ? b0 + nb : batch_size;
+        const int64_t base = fi * (batch_size + 1);
+        const int bk = order_bucket(host_offset(row_offsets, offset_type, base + b1) -
+                                        host_offset(row_offsets, offset_type, base + b0), nb);
+        bucket[k] = static_cast<unsigned char>(bk);
+        ++cnt4[k & 3][bk];
+        if (++local == per_field) {
+          local = 0;
+          ++fi;
+        }
+      }
+      // stable placement: bucket b's tiles from lane 0, then 1, 2, 3 of each group of four would
+      // not be in tile order, so take the exclusive prefix over buckets and place in tile order
+      int32_t next[kOrderBuckets];
+      int32_t run = 0;
+      for (int b = 0; b < kOrderBuckets; ++b) {
+        next[b] = run;
+        run += cnt4[0][b] + cnt4[1][b] + cnt4[2][b] + cnt4[3][b];
+      }
+      int32_t* const dst = order + kOrderHeader + lo + c0;
+      const int32_t t0 = static_cast<int32_t>(lo + c0);
+      for (int64_t k = 0; k < m; ++k) dst[next[bucket[k]]++] = t0 + static_cast<int32_t>(k);
+    }
+  }
+  order[0] = static_cast<int32_t>(n);
+  order[1] = kOrderMagic;
+  order[2] = 0;
+  order[3] = 0;
+  return CTI_EBAG_OK;
+}
+
+extern "C" int cti_ebag_fused_all_slots_ordered(const void* values, int32_t index_type, const void* val_offsets,
+                                                const void* row_offsets, int32_t offset_type, const void* weight,
+                                                int32_t table_dtype, const float* scale, void* out, int32_t out_dtype,
+                                                int64_t batch_size, int32_t num_slots, int32_t emb_dim,
+                                                int64_t max_idx, int64_t nnz, const int32_t* tile_order,
+                                                int64_t order_bytes, void* stream) {
+  clear_error();
+  if (!dtype_ok(table_dtype) && table_dtype != CTI_EBAG_I8)
+    return set_error(CTI_EBAG_EINVAL, "unknown table dtype code %d", table_dtype);
+  if (!dtype_ok(out_dtype)) return set_error(CTI_EBAG_EINVAL, "unknown output dtype code %d", out_dtype);
+  if (tile_order) {
+    if (reinterpret_cast<uintptr_t>(tile_order) % 4 != 0) return set_error(CTI_EBAG_EINVAL, "tile_order must be 4-byte aligned");
+    if (order_bytes <= 0) return set_error(CTI_EBAG_EINVAL, "order_bytes must be > 0 (got %lld)", (long long)order_bytes);
+  }
+  return run_all_slots(values, index_type, val_offsets, row_offsets, offset_type, weight,
+                       table_dtype == CTI_EBAG_I8 ? scale : nullptr, table_dtype, out, out_dtype, batch_size, num_slots,
+                       emb_dim, max_idx, nnz, stream, tile_order, order_bytes);
 }

@@ -64,7 +64,8 @@ class RepEncoder(nn.Module):
         return flat_values, val_offsets, flat_row_offsets, batch_size
 
     def pooled(self, batch: dict) -> torch.Tensor:
-        """The fused embedding step: ``[B, slot_num*emb_dim]`` in the table dtype."""
+        """The fused embedding step: ``[B, slot_num*emb_dim]`` in the table dtype (following the
+        batch's ``_tile_order`` when it carries one)."""
         flat_values, val_offsets, flat_row_offsets, batch_size = self.flat_inputs(batch)
         weight = self.emb.weight
         out = torch.empty((batch_size, self.slot_num * self.emb_dim), device=weight.device, dtype=weight.dtype)
@@ -74,7 +75,8 @@ class RepEncoder(nn.Module):
                                                       self._int8_scale, out, batch_size, self.emb_dim,
                                                       self.emb.num_embeddings - 1)
             return fused_all_slots_embedding(flat_values, val_offsets, flat_row_offsets, weight.detach(), out,
-                                             batch_size, self.emb_dim, self.emb.num_embeddings - 1)
+                                             batch_size, self.emb_dim, self.emb.num_embeddings - 1,
+                                             tile_order=batch.get("_tile_order"))
 
     def normalized(self, batch: dict) -> torch.Tensor:
         """Pooled rows after the input LayerNorm: ``[B, slot_num*emb_dim]`` in the table dtype.

@@ -196,6 +196,40 @@ def fused_all_slots_embedding_int8(
     return out
 
 
+def order_bytes(batch_size: int, num_slots: int) -> int:
+    """Bytes of a dispatch order for any launch of ``batch_size`` samples and ``num_slots`` slots."""
+    n = _capi.lib().cti_ebag_order_bytes(int(batch_size), int(num_slots))
+    if n < 0:
+        raise ValueError("batch_size and num_slots must be >= 0")
+    return n
+
+
+def make_tile_order(flat_row_offsets: torch.Tensor, batch_size: int, num_slots: int, table_dtype: torch.dtype,
+                    emb_dim: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The dispatch order of the reference-layout launch for this batch, made on the host from its
+    row offsets (a CPU int64 / int32 tensor ``[num_slots*(B+1)]``): each XCD's tiles, most rows per
+    bag first. ``table_dtype`` / ``emb_dim`` are the table's (int8 tables: ``torch.int8``). Returns
+    a CPU int32 tensor (``out`` if given, of at least ``order_bytes(B, S)`` bytes) to be moved to
+    the device with the batch and passed as ``tile_order``. No counterpart in the reference."""
+    if flat_row_offsets.device.type != "cpu" or flat_row_offsets.dtype not in (torch.int64, torch.int32):
+        raise ValueError("flat_row_offsets must be an int64 or int32 CPU tensor")
+    flat_row_offsets = flat_row_offsets.contiguous()
+    batch_size, num_slots = int(batch_size), int(num_slots)
+    if flat_row_offsets.numel() != num_slots * (batch_size + 1):
+        raise ValueError(f"flat_row_offsets has {flat_row_offsets.numel()} entries, expected "
+                         f"{num_slots} * ({batch_size} + 1)")
+    nbytes = order_bytes(batch_size, num_slots)
+    if out is None:
+        out = torch.empty((nbytes + 3) // 4, dtype=torch.int32)
+    elif out.device.type != "cpu" or out.dtype != torch.int32 or not out.is_contiguous() or out.numel() * 4 < nbytes:
+        raise ValueError(f"out must be a contiguous CPU int32 tensor of at least {nbytes} bytes")
+    tcode = _capi.I8 if table_dtype == torch.int8 else _capi.dtype_code(table_dtype)
+    _capi.check(_capi.lib().cti_ebag_order_host(flat_row_offsets.data_ptr(), _capi.index_code(flat_row_offsets.dtype),
+                                                batch_size, num_slots, tcode, int(emb_dim), out.data_ptr(),
+                                                out.numel() * 4))
+    return out
+
+
 def fused_all_slots_embedding(
     flat_values: torch.Tensor,
     val_offsets: torch.Tensor,
@@ -205,6 +239,7 @@ def fused_all_slots_embedding(
     batch_size: int,
     emb_dim: int,
     max_idx: int,
+    tile_order: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Pool every slot of a flat-layout batch into ``out[B, S*emb_dim]`` (sum, fp32 accumulate).
 
@@ -219,6 +254,10 @@ def fused_all_slots_embedding(
       batch_size        B
       emb_dim           D
       max_idx           clamp bound, V-1 in the reference (online_best/infer.py:1057)
+      tile_order        optional device int32 dispatch order of this batch (``make_tile_order``,
+                        moved with the batch; no counterpart in the reference): the launch starts
+                        each XCD's tiles with the most rows per bag, which shortens its drain. The
+                        result is the same bit for bit with or without it.
     Returns ``out``.
     """
     dev = weight.device
@@ -250,7 +289,17 @@ def fused_all_slots_embedding(
     lib = _capi.lib()
     with torch.cuda.device(dev):
         stream = _capi.current_stream_handle(dev)
-        if icode == _capi.I64 and ocode == _capi.I64:
+        if tile_order is not None:
+            _require_device_tensor("tile_order", tile_order, dev)
+            _require_contiguous("tile_order", tile_order)
+            if tile_order.dtype != torch.int32:
+                raise TypeError(f"tile_order must be int32 (got {tile_order.dtype})")
+            code = _capi.dtype_code(weight.dtype)
+            _capi.check(lib.cti_ebag_fused_all_slots_ordered(
+                flat_values.data_ptr(), icode, val_offsets.data_ptr(), flat_row_offsets.data_ptr(), ocode,
+                weight.data_ptr(), code, None, out.data_ptr(), code, batch_size, num_slots, emb_dim, max_idx,
+                flat_values.numel(), tile_order.data_ptr(), tile_order.numel() * 4, stream))
+        elif icode == _capi.I64 and ocode == _capi.I64:
             _capi.check(lib.cti_ebag_fused_all_slots(
                 flat_values.data_ptr(), val_offsets.data_ptr(), flat_row_offsets.data_ptr(),
                 weight.data_ptr(), _capi.dtype_code(weight.dtype), out.data_ptr(),
@@ -338,7 +387,9 @@ def fused_embedding(batch: dict, weight: torch.Tensor, slot_num: int, out: Optio
     batch dict holding ``_flat_values``, ``_flat_row_offsets`` and ``_val_offsets``.
 
     B is derived from the offsets length as at online_best/infer.py:1033; ``out`` is allocated
-    in the weight dtype when not given (online_best/infer.py:1050-1051).
+    in the weight dtype when not given (online_best/infer.py:1050-1051). A batch staged with a
+    dispatch order (``InputStager(order_for=...)``) carries it as ``_tile_order``; the launch
+    follows it.
     """
     flat_values = batch["_flat_values"]
     flat_row_offsets = batch["_flat_row_offsets"]
@@ -348,7 +399,7 @@ def fused_embedding(batch: dict, weight: torch.Tensor, slot_num: int, out: Optio
     if out is None:
         out = torch.empty((batch_size, slot_num * emb_dim), device=weight.device, dtype=weight.dtype)
     return fused_all_slots_embedding(flat_values, val_offsets, flat_row_offsets, weight, out,
-                                     batch_size, emb_dim, weight.shape[0] - 1)
+                                     batch_size, emb_dim, weight.shape[0] - 1, tile_order=batch.get("_tile_order"))
 
 
 def embedding_bag_pooled(

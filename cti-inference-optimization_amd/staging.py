@@ -39,15 +39,20 @@ class InputStager:
     """Ring of pinned host / device regions for flat-layout batches.
 
     ``max_nnz``, ``num_slots`` and ``max_batch`` size the regions; ``compact`` selects int32 ids
-    and offsets (else int64, as the reference sends them). Dropping the stager (or ``close()``)
+    and offsets (else int64, as the reference sends them). ``order_for=(table dtype, emb_dim)``
+    (with ``compact``) also makes each batch's dispatch order on the host from the offsets being
+    staged and sends it in the same copy as ``_tile_order``, which ``fused_embedding`` and
+    ``RepEncoder`` follow (results unchanged bit for bit). Dropping the stager (or ``close()``)
     waits for its copies; work that still reads a staged batch must be ordered before any reuse of
     that memory by the caller.
     """
 
     def __init__(self, max_nnz: int, num_slots: int, max_batch: int, device=None, depth: int = 2,
-                 compact: bool = True, threads: Optional[int] = None):
+                 compact: bool = True, threads: Optional[int] = None, order_for=None):
         if depth < 1:
             raise ValueError("depth must be >= 1")
+        if order_for is not None and not compact:
+            raise ValueError("order_for needs compact=True (the order travels as int32 in the same copy)")
         if max_nnz < 0 or num_slots < 1 or max_batch < 0:
             raise ValueError("max_nnz >= 0, num_slots >= 1 and max_batch >= 0 are required")
         if compact and max_nnz >= 2 ** 31:
@@ -60,7 +65,16 @@ class InputStager:
         self._lib = _capi.lib()
         self._code = _capi.I32 if compact else _capi.I64
         self.dtype = torch.int32 if compact else torch.int64
-        self.region_bytes = self._offset([max_nnz, num_slots * (max_batch + 1), num_slots], 3)
+        # optional fourth part: the batch's dispatch order for a table of (dtype, emb_dim), made on
+        # the host from the offsets being staged and sent in the same copy
+        self.order_for = order_for
+        self._order_elems = 0
+        if order_for is not None:
+            from .ops import order_bytes
+            self._order_elems = (order_bytes(max_batch, num_slots) + 3) // 4
+            self._order_host = torch.empty(self._order_elems, dtype=torch.int32)
+        counts = [max_nnz, num_slots * (max_batch + 1), num_slots] + ([self._order_elems] if order_for else [])
+        self.region_bytes = self._offset(counts, len(counts))
         self._h = [torch.empty(self.region_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(depth)]
         self._d = [torch.empty(self.region_bytes, dtype=torch.uint8, device=self.device) for _ in range(depth)]
         self.copy_stream = torch.cuda.Stream(self.device)  # default priority
@@ -70,15 +84,19 @@ class InputStager:
         self._next = 0
 
     def _offset(self, counts, part: int) -> int:
-        c = (ctypes.c_int64 * 3)(*counts)
-        off = self._lib.cti_ebag_stage_offset(c, 3, self._code, part)
+        c = (ctypes.c_int64 * len(counts))(*counts)
+        off = self._lib.cti_ebag_stage_offset(c, len(counts), self._code, part)
         if off < 0:
             raise ValueError(f"bad part sizes {list(counts)}")
         return off
 
     def bytes_per_batch(self, nnz: int, batch: int) -> int:
         """Bytes one batch moves host -> device."""
-        return self._offset([nnz, self.num_slots * (batch + 1), self.num_slots], 3)
+        counts = [nnz, self.num_slots * (batch + 1), self.num_slots]
+        if self.order_for is not None:
+            from .ops import order_bytes
+            counts.append((order_bytes(batch, self.num_slots) + 3) // 4)
+        return self._offset(counts, len(counts))
 
     def stage(self, batch: dict) -> dict:
         """Start moving one host batch (``_flat_values``, ``_flat_row_offsets``, ``_val_offsets``;
@@ -103,12 +121,20 @@ class InputStager:
                                "after enqueuing the work that reads it")
         self._next = (slot + 1) % self.depth
         counts = [nnz, n_off, n_vo]
-        src = (ctypes.c_void_p * 3)(*[t.data_ptr() if t.numel() else None for t in ts])
-        st = (ctypes.c_int32 * 3)(*[_capi.index_code(t.dtype) for t in ts])
-        cnt = (ctypes.c_int64 * 3)(*counts)
+        if self.order_for is not None:
+            from .ops import make_tile_order, order_bytes
+            batch_size = n_off // self.num_slots - 1
+            make_tile_order(ts[1], batch_size, self.num_slots, self.order_for[0], self.order_for[1],
+                            out=self._order_host)
+            ts = ts + [self._order_host[:(order_bytes(batch_size, self.num_slots) + 3) // 4]]
+            counts.append(ts[3].numel())
+        n = len(ts)
+        src = (ctypes.c_void_p * n)(*[t.data_ptr() if t.numel() else None for t in ts])
+        st = (ctypes.c_int32 * n)(*[_capi.index_code(t.dtype) for t in ts])
+        cnt = (ctypes.c_int64 * n)(*counts)
         self._copied[slot].synchronize()  # the previous copy out of this slot's pinned region is done
         self.copy_stream.wait_event(self._consumed[slot])  # the device region is no longer read
-        _capi.check(self._lib.cti_ebag_stage_copy(src, st, cnt, 3, self._code, self._h[slot].data_ptr(),
+        _capi.check(self._lib.cti_ebag_stage_copy(src, st, cnt, n, self._code, self._h[slot].data_ptr(),
                                                   self.region_bytes, self._d[slot].data_ptr(), self.threads,
                                                   self.copy_stream.cuda_stream))
         self._copied[slot].record(self.copy_stream)
@@ -116,7 +142,7 @@ class InputStager:
         self._in_use[slot] = True
         out = {"_stage_slot": slot}
         d = self._d[slot]
-        for k, c, part in zip(_PARTS, counts, range(3)):
+        for k, c, part in zip(_PARTS + ("_tile_order",), counts, range(n)):
             off = self._offset(counts, part)
             out[k] = d[off:off + c * (4 if self.compact else 8)].view(self.dtype)
         return out

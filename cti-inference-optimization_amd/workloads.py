@@ -1,6 +1,6 @@
 """Seeded synthetic workloads of the fused embedding-bag path (no dataset ships with the path).
 
-Five shapes, all with 28 fields in the flat field-major layout (values + global offsets):
+Six shapes, all with 28 fields in the flat field-major layout (values + global offsets):
 
   small-fp32   fp32 tables 10,000 x 64, B=256, Poisson(3) lengths clipped to [0, 32] plus
                ~10% empty bags, uniform ids, sum
@@ -13,6 +13,10 @@ Five shapes, all with 28 fields in the flat field-major layout (values + global 
                lognormal lengths (median 64) clipped to [1, 2048]; 5% empty bags; sum
   lazy-32k     bf16 tables 4,000,000 x 128, B=32768 = 8 sub-batches of 4096 with Poisson
                lengths of mean 1, 4 or 16, concatenated field by field; Zipf(0.8) ids; mean
+  reference-5m the reference's own shape: one shared bf16 table 5,000,000 x 512 (5.12 GB) for
+               all 28 slots, B=4096, lengths and ids as bf16-2m, sum
+
+Five shapes come from the path's benchmark configurations; reference-5m is the reference's own.
 
 Choices the shape descriptions leave open: rows ~ N(0, 0.01); lengths "geometric(mean 8)" are
 Geometric(p=1/9) - 1 on {0, 1, ...}; the small config forces each bag empty with q = 0.0528 on
@@ -153,6 +157,13 @@ def bf16_2m(seed: int = 0, batch: int = 4096, vocab: int = 2_000_000) -> Workloa
     return _geometric_zipf("bf16-2m", seed, batch, vocab, 128, torch.bfloat16, torch.bfloat16, "mean")
 
 
+def reference_5m(seed: int = 0, batch: int = 4096, vocab: int = 5_000_000) -> Workload:
+    """The reference's own table shape: 28 slots over one shared bf16 nn.Embedding(5,000,000,
+    512) (online_best/infer.py:948, :2757-2771), summed (:819-827); lengths and Zipf(1.1) ids as
+    bf16-2m, each slot with its own popularity order over the shared rows."""
+    return _geometric_zipf("reference-5m", seed, batch, vocab, 512, torch.bfloat16, torch.bfloat16, "sum")
+
+
 def hetero_bf16(seed: int = 0, batch: int = 8192, vocab_max: int = 5_000_000) -> Workload:
     lengths, ids, dims, vocab = [], [], [], []
     for f, rng in enumerate(_streams(seed)):
@@ -201,6 +212,7 @@ CONFIGS = {
     "bf16-2m": bf16_2m,
     "hetero-bf16": hetero_bf16,
     "lazy-32k": lazy_32k,
+    "reference-5m": reference_5m,
 }
 
 
@@ -209,13 +221,20 @@ def make(name: str, seed: int = 0, **kw) -> Workload:
 
 
 def make_tables(wl: Workload, device, seed: int = 0) -> List[torch.Tensor]:
-    """One table per field, rows ~ N(0, 0.01), in the workload's table dtype.
+    """One table per field, rows ~ N(0, 0.01), in the workload's table dtype (reference-5m: one
+    table shared by all fields).
 
     The small config draws its rows on the host (numpy, seed) so that the same tables can be
     rebuilt anywhere; the large ones are drawn on the device (torch generator, seed + field).
     """
     device = torch.device(device)
     tables = []
+    if wl.name == "reference-5m":  # one table shared by every slot, as the reference's nn.Embedding
+        g = torch.Generator(device=device)
+        g.manual_seed(seed * 1000)
+        t = torch.empty((wl.vocab[0], wl.dims[0]), dtype=wl.table_dtype, device=device)
+        t.normal_(0.0, 0.01, generator=g)
+        return [t] * wl.num_fields
     if wl.name == "small-fp32":
         rng = np.random.default_rng(seed)
         for f in range(wl.num_fields):

@@ -268,6 +268,35 @@ int cti_ebag_fused_all_slots_typed(const void* values, int32_t index_type, const
                                    int64_t nnz, void* stream);
 
 /*
+ * Dispatch order of a reference-layout launch, made on the HOST where the batch's offsets are
+ * produced (no counterpart in the reference). The reference's Triton launch runs one program per
+ * bag (online_best/infer.py:1053); here a launch ends with a drain when tiles of long bags start
+ * late. An order lists each XCD's tiles most rows per bag first, which removes most of it; a
+ * collate or staging pass that already holds the offsets makes it at no cost to the GPU, and the
+ * launch then follows it (cti_ebag_fused_all_slots_ordered). Results are the same bit for bit
+ * with or without an order, and with an order made for another batch.
+ *   row_offsets  HOST [num_slots*(B+1)] of `offset_type` (I64 / I32), as the launch will read
+ *   table_dtype, emb_dim   the launch's table (they fix how many bags a tile holds)
+ *   order        HOST int32 buffer of order_bytes >= cti_ebag_order_bytes(batch_size, num_slots)
+ * CTI_EBAG_EUNSUPPORTED for rows that take the element-wise kernel (not whole 16-byte vectors,
+ * or wider than 4 KB) and for more than 64 slots.
+ */
+int cti_ebag_order_host(const void* row_offsets, int32_t offset_type, int64_t batch_size, int32_t num_slots,
+                        int32_t table_dtype, int32_t emb_dim, int32_t* order, int64_t order_bytes);
+
+/*
+ * cti_ebag_fused_all_slots_typed following a dispatch order (NULL = none): `tile_order` is a
+ * DEVICE copy of what cti_ebag_order_host wrote (order_bytes bytes). An order made for a launch of
+ * another tile count is detected on the device and not followed; an order for the same tile count
+ * but other offsets only changes which tiles start first.
+ */
+int cti_ebag_fused_all_slots_ordered(const void* values, int32_t index_type, const void* val_offsets,
+                                     const void* row_offsets, int32_t offset_type, const void* weight,
+                                     int32_t table_dtype, const float* scale, void* out, int32_t out_dtype,
+                                     int64_t batch_size, int32_t num_slots, int32_t emb_dim, int64_t max_idx,
+                                     int64_t nnz, const int32_t* tile_order, int64_t order_bytes, void* stream);
+
+/*
  * The reference-layout pooling with the encoder's input LayerNorm fused into the writer
  * (online_best/infer.py:1050-1076: the pooled block `fused_embs` [B, S*D] and
  * layernorm_forward_kernel over its rows, :829-858): out[b] = LayerNorm(pool(b)), where pool(b)

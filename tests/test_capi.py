@@ -4,6 +4,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch
 
@@ -392,3 +393,64 @@ def test_narrow_ids_in_a_forked_child(pkg):
             os._exit(code)
     _, status = os.waitpid(pid, 0)
     assert os.WIFEXITED(status) and os.WEXITSTATUS(status) == 0
+
+
+def _ref_offsets(rng, S, B, max_len):
+    L = rng.integers(0, max_len + 1, size=(S, B))
+    L[:, ::9] = rng.integers(60, 200, size=L[:, ::9].shape)
+    ro = np.zeros((S, B + 1), np.int64)
+    np.cumsum(L, axis=1, out=ro[:, 1:])
+    return ro
+
+
+@pytest.mark.parametrize("dt,D,nb", [(torch.bfloat16, 128, 8), (torch.float32, 64, 8), (torch.bfloat16, 512, 2),
+                                     (torch.float32, 1024, 2), (torch.bfloat16, 16, 64), (torch.int8, 128, 8)])
+@pytest.mark.parametrize("S,B", [(28, 4096), (3, 777), (1, 5), (64, 100)])
+def test_host_order_is_a_sorted_permutation(pkg, dt, D, nb, S, B):
+    """cti_ebag_order_host (host code): header, every XCD range a permutation of itself, each chunk
+    of 2048 tiles ordered by rows per bag (most first, capped at 63) and stable within a bucket,
+    for int64 and int32 offsets alike."""
+    rng = np.random.default_rng(S * 1000 + B)
+    ro = _ref_offsets(rng, S, B, 30)
+    a = pkg.make_tile_order(torch.from_numpy(ro.reshape(-1)), B, S, dt, D)
+    b = pkg.make_tile_order(torch.from_numpy(ro.reshape(-1).astype(np.int32)), B, S, dt, D)
+    o = a.numpy()
+    tpf = (B + nb - 1) // nb
+    n = S * tpf
+    assert np.array_equal(o[:4 + n], b.numpy()[:4 + n])  # entries past the order are not written
+    assert o[0] == n and o[1] == 0x4F524452 and o[2] == 0 and o[3] == 0
+    perm = o[4:4 + n]
+    q, r = n >> 3, n & 7
+    for x in range(8):
+        lo = x * (q + 1) if x < r else r * (q + 1) + (x - r) * q
+        cnt = q + (1 if x < r else 0)
+        seg = perm[lo:lo + cnt]
+        assert np.array_equal(np.sort(seg), np.arange(lo, lo + cnt))
+        for c0 in range(0, cnt, 2048):
+            part = seg[c0:c0 + 2048]
+            assert np.array_equal(np.sort(part), np.arange(lo + c0, lo + c0 + len(part)))
+            fi = part // tpf
+            b0 = (part - fi * tpf) * nb
+            b1 = np.minimum(b0 + nb, B)
+            per_bag = np.clip((ro[fi, b1] - ro[fi, b0]) // nb, 0, 63)
+            assert (np.diff(per_bag) <= 0).all()
+            same = np.diff(per_bag) == 0
+            assert (np.diff(part)[same] > 0).all()  # stable: tile order inside a bucket
+
+
+def test_host_order_rejections(pkg):
+    c = pkg._capi
+    lib = c.lib()
+    ro = torch.zeros(3 * 11, dtype=torch.int64)
+    buf = torch.zeros(64, dtype=torch.int32)
+    call = lambda *a: lib.cti_ebag_order_host(*a)  # noqa: E731
+    assert call(ro.data_ptr(), c.I64, 10, 3, c.BF16, 128, buf.data_ptr(), 36) == c.EINVAL  # 6 tiles need 40 bytes
+    assert call(ro.data_ptr(), c.I64, 10, 3, c.BF16, 128, buf.data_ptr(), 40) == c.OK
+    assert call(ro.data_ptr(), c.I64, 10, 3, c.BF16, 100, buf.data_ptr(), 1 << 20) == c.EUNSUPPORTED  # element-wise
+    assert call(ro.data_ptr(), 7, 10, 3, c.BF16, 128, buf.data_ptr(), 1 << 20) == c.EINVAL
+    assert call(None, c.I64, 10, 3, c.BF16, 128, buf.data_ptr(), 1 << 20) == c.EINVAL
+    assert call(ro.data_ptr(), c.I64, 0, 3, c.BF16, 128, buf.data_ptr(), 1 << 20) == c.EINVAL
+    big = torch.zeros(65 * 11, dtype=torch.int64)
+    assert call(big.data_ptr(), c.I64, 10, 65, c.BF16, 128, buf.data_ptr(), 1 << 20) == c.EUNSUPPORTED
+    with pytest.raises(ValueError):
+        pkg.make_tile_order(torch.zeros(7, dtype=torch.int64), 10, 3, torch.bfloat16, 128)

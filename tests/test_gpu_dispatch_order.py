@@ -249,3 +249,88 @@ def test_random_shapes_ordered_equal_unordered(pkg, dev, seed):
         assert not tiled and e.status == pkg._capi.EUNSUPPORTED, e  # refused before any launch
     else:
         assert tiled, "a job of the generic kernel took a dispatch order"
+
+
+# ---- orders made on the host where the offsets are produced (cti_ebag_order_host) -------------
+HOST_SHAPES = [  # (table dtype, dim, slots, batch, max bag length)
+    ("bf16", 128, 28, 700, 60),
+    ("f32", 64, 5, 333, 300),
+    ("bf16", 512, 3, 100, 30),
+    ("f32", 1024, 2, 50, 20),
+    ("bf16", 128, 1, 5, 48),
+]
+
+
+def _reference_batch(rng, S, B, max_len, long_every=0):
+    L = rng.integers(0, max_len + 1, size=(S, B))
+    if long_every:
+        L[:, ::long_every] = rng.integers(100, 250, size=L[:, ::long_every].shape)
+    ro = np.zeros((S, B + 1), np.int64)
+    np.cumsum(L, axis=1, out=ro[:, 1:])
+    vo = np.concatenate([[0], np.cumsum(L.sum(axis=1))[:-1]]).astype(np.int64)
+    return make_ids(rng, int(L.sum()), V), ro.reshape(-1), vo
+
+
+@pytest.mark.parametrize("shape", range(len(HOST_SHAPES)))
+def test_host_order_launch_equals_plain(pkg, dev, shape):
+    """The drop-in launch following a host-made order equals the plain launch bit for bit, for its
+    own batch, for the order of another batch of the same size, and with an order made for
+    another batch size (not followed); bags of at most 48 rows also equal the oracle."""
+    tdt, D, S, B, max_len = HOST_SHAPES[shape]
+    print(f"host order: {tdt} D={D} S={S} B={B}", flush=True)
+    rng = np.random.default_rng(200 + shape)
+    table = make_table(rng, V, D, tdt)
+    w = to_dev(table, tdt, dev)
+    tdt_t = {"bf16": torch.bfloat16, "f32": torch.float32}[tdt]
+    batches = [_reference_batch(rng, S, B, max_len, long_every=5 if k == 1 else 0) for k in range(3)]
+    small = _reference_batch(rng, S, max(1, B // 3), max_len)
+    for k, (v, ro, vo) in enumerate(batches):
+        dv, dro, dvo = (torch.from_numpy(x).to(dev) for x in (v, ro, vo))
+        plain = torch.empty((B, S * D), dtype=tdt_t, device=dev)
+        pkg.fused_all_slots_embedding(dv, dvo, dro, w, plain, B, D, V - 1)
+        own = pkg.make_tile_order(torch.from_numpy(ro), B, S, tdt_t, D)
+        other = pkg.make_tile_order(torch.from_numpy(batches[(k + 1) % 3][1]), B, S, tdt_t, D)
+        # an order made for another batch size, in a buffer large enough for this launch (a smaller
+        # buffer is refused on the host: the launch would read past it)
+        foreign = pkg.make_tile_order(torch.from_numpy(small[1]), max(1, B // 3), S, tdt_t, D,
+                                      out=torch.zeros(pkg.order_bytes(B, S) // 4, dtype=torch.int32))
+        short = torch.from_numpy(own.numpy()[:4].copy())  # the header alone: smaller than any launch needs
+        with pytest.raises(pkg.EbagError, match="order buffers"):
+            pkg.fused_all_slots_embedding(dv, dvo, dro, w, torch.empty_like(plain), B, D, V - 1,
+                                          tile_order=short.to(dev))
+        for order in (own, other, foreign):
+            got = torch.empty_like(plain)
+            pkg.fused_all_slots_embedding(dv, dvo, dro, w, got, B, D, V - 1, tile_order=order.to(dev))
+            torch.cuda.synchronize()
+            assert torch.equal(_bits(got), _bits(plain))
+        if int(np.diff(ro.reshape(S, B + 1), axis=1).max(initial=0)) <= 48:
+            want = orc.pool_c(v, ro, [table] * S, tdt, "sum", tdt, batch=B, val_base=vo)
+            assert np.array_equal(to_np(plain, tdt), want)
+
+
+def test_stager_with_orders_matches_oracle(pkg, dev):
+    """InputStager(order_for=...) sends each batch's host-made order in the same copy; the staged,
+    ordered pooling equals the oracle's pooling of the host batch bit for bit."""
+    S, D = 28, 128
+    rng = np.random.default_rng(17)
+    table = make_table(rng, V, D, "bf16")
+    w = to_dev(table, "bf16", dev)
+    hosts = []
+    for k in range(5):
+        B = int(rng.integers(1, 300))
+        v, ro, vo = _reference_batch(rng, S, B, 40)
+        hosts.append(({"_flat_values": torch.from_numpy(v), "_flat_row_offsets": torch.from_numpy(ro),
+                       "_val_offsets": torch.from_numpy(vo)}, B))
+    max_nnz = max(h["_flat_values"].numel() for h, _ in hosts)
+    stager = pkg.InputStager(max_nnz, S, 300, dev, depth=2, order_for=(torch.bfloat16, D))
+    outs = []
+    for h, B in hosts:
+        staged = pkg.move_model_inputs_to_device(h, dev, S, stager=stager)
+        assert staged["_tile_order"].dtype == torch.int32
+        outs.append(pkg.fused_embedding(staged, w, S).clone())
+        stager.release(staged)
+    torch.cuda.synchronize()
+    for (h, B), got in zip(hosts, outs):
+        want = orc.pool_c(h["_flat_values"].numpy(), h["_flat_row_offsets"].numpy(), [table] * S, "bf16", "sum",
+                          batch=B, val_base=h["_val_offsets"].numpy())
+        assert np.array_equal(to_np(got, "bf16"), want)
