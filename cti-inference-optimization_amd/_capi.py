@@ -87,6 +87,11 @@ SIGNATURES = {
         [_P, _I32, _I64, _P, _I64, _I32, ctypes.POINTER(Table), _I32, _I32, _P, _I32, _I64, _P, _I64,
          ctypes.POINTER(Options), _P],
     ),
+    "cti_ebag_forward_static": (
+        ctypes.c_int,
+        [_P, _I32, _I64, _P, _I64, _I32, ctypes.POINTER(Table), _I32, _I32, _P, _I32, _I64,
+         ctypes.POINTER(Options), _P],
+    ),
     "cti_ebag_workspace_bytes": (ctypes.c_int64, [_I64, _I32]),
     "cti_ebag_order_bytes": (ctypes.c_int64, [_I64, _I32]),
     "cti_ebag_pack_slots": (ctypes.c_int, [_PP, _PP, _PI64, _I32, _I64, _P, _P, _P, _P, _P]),

@@ -16,7 +16,8 @@
  *
  * Conventions
  *   - Every pointer argument is a device pointer unless stated otherwise ("host" below).
- *   - Nothing here allocates device memory, synchronises the host, or throws. Work is
+ *   - Nothing here allocates device memory, synchronises the host, or throws (the one static
+ *     device array of cti_ebag_forward_static is part of the loaded library). Work is
  *     enqueued on `stream` (a hipStream_t; NULL = the default stream) and runs asynchronously.
  *   - Return value: CTI_EBAG_OK (0) or a negative CTI_EBAG_E* code; the message of the last
  *     failure on the calling host thread is returned by cti_ebag_last_error().
@@ -168,6 +169,25 @@ int cti_ebag_forward(const void* values, int32_t index_type, int64_t nnz, const 
                      int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
                      int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
                      const cti_ebag_options* opts, void* stream);
+
+/*
+ * Allocation-free form of cti_ebag_forward. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops, hosts
+ * that forbid allocation). Arguments and results are cti_ebag_forward's, without the workspace:
+ * the length-binning lists live in a static device array of CTI_EBAG_STATIC_WORKSPACE_BYTES
+ * inside the library, one per GPU, held until the process ends. With opts->use_bins, a job whose
+ * cti_ebag_workspace_bytes(batch_size, num_fields) exceeds that size (batch_size *
+ * min(num_fields, 64) > 1,398,090 bags) is rejected with CTI_EBAG_EWORKSPACE before any launch.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller. The first call on a
+ * device looks up that device's copy and zeroes its list counters on `stream`; every call leaves
+ * them zero again.
+ */
+#define CTI_EBAG_STATIC_WORKSPACE_BYTES (32ll << 20)
+int cti_ebag_forward_static(const void* values, int32_t index_type, int64_t nnz, const int64_t* offsets,
+                            int64_t batch_size, int32_t num_fields, const cti_ebag_table* tables,
+                            int32_t table_dtype, int32_t pooling, void* out, int32_t out_dtype,
+                            int64_t out_row_stride, const cti_ebag_options* opts, void* stream);
 
 /* Bytes of device workspace cti_ebag_forward needs with opts->use_bins = 1
  * (256 + 24 * batch_size * min(num_fields, 64): list counters, then the field / sample and the
