@@ -450,33 +450,39 @@ def bench_reference(args, pkg, dev):
         v, vo, ro = batches[i % n]
         pkg.fused_all_slots_embedding_layernorm(v, vo, ro, weight, out, B, D, V - 1, gamma, beta, 1e-5)
 
+    legs = set(args.legs.split(","))
     us = {}
-    log("drop-in pooling")
-    us["pool"] = timed(pool) * 1e6
-    log("pooling + LayerNorm fused")
-    us["pool_layernorm_fused"] = timed(fused) * 1e6
+    if "pool" in legs:
+        log("drop-in pooling")
+        us["pool"] = timed(pool) * 1e6
+    if "fused" in legs:
+        log("pooling + LayerNorm fused")
+        us["pool_layernorm_fused"] = timed(fused) * 1e6
 
     def pool_int8(i):
         v, vo, ro = batches[i % n]
         pkg.fused_all_slots_embedding_int8(v, vo, ro, q, sc, out, B, D, V - 1)
 
-    log("quantising the table to int8")
-    q, sc = pkg.quantize_embedding_int8(weight)
-    log("int8 pooling")
-    us["pool_int8"] = timed(pool_int8) * 1e6
-    del q, sc
-    torch.cuda.empty_cache()
+    if "int8" in legs:
+        log("quantising the table to int8")
+        q, sc = pkg.quantize_embedding_int8(weight)
+        log("int8 pooling")
+        us["pool_int8"] = timed(pool_int8) * 1e6
+        del q, sc
+        torch.cuda.empty_cache()
 
-    # the addressing paths on identical batches: ids < 4,194,303 (so no clamp differs)
-    V4 = (1 << 32) // (D * 2) - 1
-    log("addressing paths: index sets over 4,194,303 rows")
-    wl4 = [W.make("reference-5m", seed=s, vocab=V4) for s in range(1, args.sets + 1)]
-    b4 = [reference_layout(wl, dev) for wl in wl4]
-    us["pool_64bit_addresses_ids_below_4gib"] = timed(lambda i: pool(i, weight, b4)) * 1e6
-    del weight
-    torch.cuda.empty_cache()
-    w4 = torch.empty((V4, D), dtype=torch.bfloat16, device=dev).normal_(0.0, 0.01, generator=g)
-    us["pool_buffer_path_table_below_4gib"] = timed(lambda i: pool(i, w4, b4)) * 1e6
+    wl4 = []
+    if "addressing" in legs:
+        # the addressing paths on identical batches: ids < 4,194,303 (so no clamp differs)
+        V4 = (1 << 32) // (D * 2) - 1
+        log("addressing paths: index sets over 4,194,303 rows")
+        wl4 = [W.make("reference-5m", seed=s, vocab=V4) for s in range(1, args.sets + 1)]
+        b4 = [reference_layout(wl, dev) for wl in wl4]
+        us["pool_64bit_addresses_ids_below_4gib"] = timed(lambda i: pool(i, weight, b4)) * 1e6
+        del weight
+        torch.cuda.empty_cache()
+        w4 = torch.empty((V4, D), dtype=torch.bfloat16, device=dev).normal_(0.0, 0.01, generator=g)
+        us["pool_buffer_path_table_below_4gib"] = timed(lambda i: pool(i, w4, b4)) * 1e6
 
     def alg_bytes(wl, tb=2, extra=0):
         # each lookup's row, ids, the reference layout's offsets, the output
@@ -484,8 +490,10 @@ def bench_reference(args, pkg, dev):
 
     pool_bytes = float(np.mean([alg_bytes(wl) for wl in wls]))
     int8_bytes = float(np.mean([alg_bytes(wl, 1, 4) for wl in wls]))
-    b4_bytes = float(np.mean([alg_bytes(wl) for wl in wl4]))
     fused_bytes = pool_bytes + 2 * F * D * 2
+    if "pool" not in legs:
+        print(json.dumps({"us_per_step": us}), flush=True)
+        return
     t = us["pool"] / 1e6
     rec = {
         "metric": "pooled bags/sec at the reference's own table shape (one shared bf16 [5e6, 512] table, 28 slots)",
@@ -497,16 +505,22 @@ def bench_reference(args, pkg, dev):
                    "nnz_mean": float(np.mean([wl.nnz for wl in wls]))},
         "us_per_step": us,
         "roofline": roofline(pool_bytes / t / 1e9, pool_bytes, t, "pool_kernel", ("reference-5m", "pool_kernel")),
-        "roofline_fused_layernorm": roofline(fused_bytes / (us["pool_layernorm_fused"] / 1e6) / 1e9, fused_bytes,
-                                             us["pool_layernorm_fused"] / 1e6, "pool_norm_kernel",
-                                             ("reference-5m", "pool_norm_kernel")),
-        "roofline_int8": roofline(int8_bytes / (us["pool_int8"] / 1e6) / 1e9, int8_bytes, us["pool_int8"] / 1e6,
-                                  "pool_kernel", ("reference-5m-int8", "pool_kernel")),
-        "addressing": {"bytes_per_launch": b4_bytes,
-                       "frac_64bit": b4_bytes / (us["pool_64bit_addresses_ids_below_4gib"] / 1e6) / 1e9 / HBM_PEAK_GBS,
-                       "frac_buffer": b4_bytes / (us["pool_buffer_path_table_below_4gib"] / 1e6) / 1e9 / HBM_PEAK_GBS},
         "cpu_baseline": None,
     }
+    if "fused" in legs:
+        tf = us["pool_layernorm_fused"] / 1e6
+        rec["roofline_fused_layernorm"] = roofline(fused_bytes / tf / 1e9, fused_bytes, tf, "pool_norm_kernel",
+                                                   ("reference-5m", "pool_norm_kernel"))
+    if "int8" in legs:
+        ti = us["pool_int8"] / 1e6
+        rec["roofline_int8"] = roofline(int8_bytes / ti / 1e9, int8_bytes, ti, "pool_kernel",
+                                        ("reference-5m-int8", "pool_kernel"))
+    if wl4:
+        b4_bytes = float(np.mean([alg_bytes(wl) for wl in wl4]))
+        rec["addressing"] = {
+            "bytes_per_launch": b4_bytes,
+            "frac_64bit": b4_bytes / (us["pool_64bit_addresses_ids_below_4gib"] / 1e6) / 1e9 / HBM_PEAK_GBS,
+            "frac_buffer": b4_bytes / (us["pool_buffer_path_table_below_4gib"] / 1e6) / 1e9 / HBM_PEAK_GBS}
     print(json.dumps(rec), flush=True)
 
 
@@ -715,16 +729,19 @@ def main():
                     help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
                          "step end to end from host batches")
     ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
-    ap.add_argument("--dispatch-order", choices=["auto", "on", "off"], default="auto",
-                    help="on: each step also sorts the next batch's tiles (most rows per bag first) and follows "
-                         "the order the previous step made; auto: on for the workloads where that was measured "
-                         "to pay (%s) without --bins" % ", ".join(sorted(ORDERED_BY_DEFAULT)))
+    ap.add_argument("--legs", default="pool,fused,int8,addressing",
+                    help="--stage reference: which of pool, fused, int8, addressing to time")
+    ap.add_argument("--dispatch-order", choices=["auto", "host", "launch", "off"], default="auto",
+                    help="host: each batch carries its tile order (most rows per bag first in each XCD's share), "
+                         "made on the host from its offsets where the batch is produced; launch: each step also "
+                         "sorts the next batch's tiles on the device and follows the order the previous step made; "
+                         "auto: host for the workloads where ordering was measured to pay (%s) without --bins"
+                         % ", ".join(sorted(ORDERED_BY_DEFAULT)))
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy 1 GiB device-to-device 3 times (scales rocprofv3 FETCH/WRITE_SIZE) and exit")
     args = ap.parse_args()
     if args.dispatch_order == "auto":
-        args.dispatch_order = "on" if args.workload in ORDERED_BY_DEFAULT and not args.bins else "off"
-    args.dispatch_order = args.dispatch_order == "on"
+        args.dispatch_order = "host" if args.workload in ORDERED_BY_DEFAULT and not args.bins else "off"
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -774,7 +791,13 @@ def main():
     plan = pkg.PooledEmbedding(pooled_tables, pooling=wl0.pooling, out_dtype=wl0.out_dtype,
                                long_threshold=args.long_threshold, use_bins=args.bins,
                                block_threshold=args.block_threshold, max_batch=wl0.batch,
-                               split_threshold=args.split_threshold, dispatch_order=args.dispatch_order)
+                               split_threshold=args.split_threshold, dispatch_order=args.dispatch_order == "launch")
+    orders = None
+    if args.dispatch_order == "host":
+        # each batch's order, made on the host from its offsets as its producer would make it
+        tdt = torch.int8 if args.int8 else wl0.table_dtype
+        orders = [pkg.make_tile_order(torch.from_numpy(wl.offsets), wl.batch, wl.num_fields, tdt, wl.dims[0]).to(dev)
+                  for wl in wls]
     out = torch.empty((wl0.batch, sum(wl0.dims)), dtype=wl0.out_dtype, device=dev)
     if args.stage == "layernorm":
         return bench_layernorm(args, pkg, plan, inputs, wl0, dev)
@@ -784,8 +807,10 @@ def main():
 
     def step(i):
         v, o = inputs[i % args.sets]
-        if args.dispatch_order:
+        if args.dispatch_order == "launch":
             plan(v, o, out, next_offsets=inputs[(i + 1) % args.sets][1])
+        elif orders is not None:
+            plan(v, o, out, tile_order=orders[i % args.sets])
         else:
             plan(v, o, out)
 
@@ -856,16 +881,19 @@ def main():
         "dtype": "i8" if args.int8 else {torch.bfloat16: "bf16", torch.float32: "f32",
                                           torch.float16: "f16"}[wl0.table_dtype],
         "data": f"synthetic: {args.sets} seeded index sets rotated, random N(0, 0.01) tables"
-                + (", row-quantised to int8 on the device" if args.int8 else ""),
+                + (", row-quantised to int8 on the device" if args.int8 else "")
+                + ("; each batch carries its tile order, made on the host from its offsets" if orders is not None
+                   else ""),
         "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}", "batch": wl0.batch,
                    "fields": wl0.num_fields, "dims": sorted(set(wl0.dims)), "pooling": wl0.pooling,
                    "nnz_mean": float(np.mean([wl.nnz for wl in wls])), "index_sets": args.sets,
                    "length_binning": bool(args.bins), "int8_tables": bool(args.int8),
-                   "dispatch_order": bool(args.dispatch_order)},
+                   "dispatch_order": args.dispatch_order},
         "roofline": roofline(achieved, used_bytes, mean_launch_s, kernel_name,
                              (args.workload + ("-int8" if args.int8 else ""), prof_kernel,
-                              ("hbm_bytes_per_launch",) if args.dispatch_order
-                              else ("hbm_bytes_per_launch_order_off", "hbm_bytes_per_launch")),
+                              {"host": ("hbm_bytes_per_launch",),
+                               "launch": ("hbm_bytes_per_launch_order_launch", "hbm_bytes_per_launch"),
+                               "off": ("hbm_bytes_per_launch_order_off", "hbm_bytes_per_launch")}[args.dispatch_order]),
                              compulsory_bytes_per_launch=used_comp),
         "cpu_baseline": cpu,
     }

@@ -122,7 +122,7 @@ SIGNATURES = {
         [_PP, ctypes.POINTER(ctypes.c_int32), _PI64, _I32, _I32, _P, _I64, _P, _I32, _P],
     ),
     "cti_ebag_stage_offset": (ctypes.c_int64, [_PI64, _I32, _I32, _I32]),
-    "cti_ebag_order_host": (ctypes.c_int, [_P, _I32, _I64, _I32, _I32, _I32, _P, _I64]),
+    "cti_ebag_order_host": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _I32, _I32, _P, _I64, _I32]),
     "cti_ebag_fused_all_slots_ordered": (
         ctypes.c_int,
         [_P, _I32, _P, _P, _I32, _P, _I32, _P, _P, _I32, _I64, _I32, _I32, _I64, _I64, _P, _I64, _P],

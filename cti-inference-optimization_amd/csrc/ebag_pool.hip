@@ -504,10 +504,9 @@ __device__ __forceinline__ void bin_handoff(const PoolParams& p) {
 // [kOrderHeader + position] = tile. A launch follows an order only if [0] and [1] match it, and
 // takes its own position for any entry outside its tiles, so no buffer can make it read or write
 // out of bounds; an order written here for any launch of as many tiles is a permutation of them.
-constexpr int32_t kOrderMagic = 0x4f524452;
-constexpr int kOrderHeader = 4;
-constexpr int kOrderChunk = 2048;   // an XCD range is sorted in chunks of this many tiles
-constexpr int kOrderBuckets = 64;   // rows per bag 63, 62, ..., 0 (more count as 63)
+// kOrderMagic, kOrderHeader, kOrderChunk (an XCD range is sorted in chunks of this many tiles)
+// and kOrderBuckets (rows per bag 63, 62, ..., 0; more count as 63) are shared with the host
+// builder (ebag_internal.h).
 constexpr int kOrderUnroll = 8;     // tiles per lane whose offsets are loaded together
 static_assert(kOrderBuckets == kWave, "one bucket per lane in the prefix sum");
 
@@ -663,8 +662,12 @@ __global__ void __launch_bounds__(kMainThreads) pool_mixed_kernel(const PoolPara
 // wavefront for longer bags) and writes each result, rounded to the output type, into an LDS
 // copy of the row; the workgroup then normalises that row (fp32 mean and variance, fixed
 // reduction order) and stores it once.
-constexpr int kFusedWaves = 4;
-constexpr int kFusedBagsPerWave = 32;  // samples per workgroup * ceil(fields / kFusedWaves) <= 32
+constexpr int kFusedBagsPerWave = 32;  // samples per workgroup * ceil(fields / waves) <= 32
+
+// Wavefronts per fused workgroup for rows of `lanes` lanes (one 16-byte vector per lane).
+// Measured (reference shape: 28 slots of 1 KiB rows, B = 4096; bf16-2m shape: 256-byte rows):
+// 1 KiB rows 4 / 8 / 16 wavefronts 162.5 / 149.3 / 176.2 us; 256-byte rows 4 / 8: 40.7 / 50.8 us.
+constexpr int fused_waves(int lanes) { return lanes >= 64 ? 8 : 4; }
 
 struct FusedLds {  // one per wavefront
   unsigned int ids[kWave];
@@ -683,12 +686,11 @@ struct FusedNorm {
 // wavefronts of a fused workgroup pool independently, so no workgroup barrier is used here.
 __device__ __forceinline__ void wave_sync() { __builtin_amdgcn_wave_barrier(); }
 
-template <typename TT, typename PT, int LANES, int SPW, bool BUF>
-__global__ void __launch_bounds__(kFusedWaves * kWave) pool_norm_kernel(const PoolParams p, const FusedNorm fn) {
+template <typename TT, typename PT, int LANES, int SPW, bool BUF, int W = fused_waves(LANES)>
+__global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p, const FusedNorm fn) {
   using S = Shape<TT, LANES, 1>;
   constexpr int U = S::U;
   constexpr int R = S::R;
-  constexpr int W = kFusedWaves;
   extern __shared__ uint4 s_row_raw[];  // the output rows: SPW * F * D elements of TT
   __shared__ FusedLds s_w[W];
   __shared__ float s_red[W];
@@ -1585,7 +1587,7 @@ namespace {
 
 template <typename TT, typename PT, int LANES>
 hipError_t launch_fused(const PoolParams& p, const FusedNorm& fn, int spw, size_t row_lds, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((p.batch + spw - 1) / spw)), block(kFusedWaves * kWave);
+  const dim3 grid(static_cast<unsigned>((p.batch + spw - 1) / spw)), block(fused_waves(LANES) * kWave);
   const size_t lds = row_lds * spw;
   switch (spw * 2 + (p.buffer_ok ? 1 : 0)) {
     case 2: hipLaunchKernelGGL((pool_norm_kernel<TT, PT, LANES, 1, false>), grid, block, lds, s, p, fn); break;
@@ -1615,8 +1617,9 @@ constexpr int kFusedSamples = 2;  // measured: 1 / 2 / 4 samples per workgroup 4
 // Samples per fused workgroup: up to kFusedSamples, while every wavefront's bags fit
 // its lanes' bookkeeping and the LDS rows stay within kFusedLdsMax.
 constexpr int64_t kFusedLdsMax = 64 * 1024;
-int fused_samples(int num_slots, int64_t row_out_bytes) {
-  const int per_wave = (num_slots + kFusedWaves - 1) / kFusedWaves;
+int fused_samples(int num_slots, int64_t row_out_bytes, int lanes) {
+  const int waves = fused_waves(lanes);
+  const int per_wave = (num_slots + waves - 1) / waves;
   int spw = kFusedSamples;
   while (spw > 1 && (spw * per_wave > kFusedBagsPerWave || spw * row_out_bytes > kFusedLdsMax / 2)) spw /= 2;
   return spw;
@@ -1705,7 +1708,7 @@ extern "C" int cti_ebag_fused_all_slots_layernorm(const void* values, int32_t in
   fn.beta = beta;
   fn.eps = eps;
   const size_t row_lds = static_cast<size_t>(row_bytes * num_slots);
-  const int spw = fused_samples(num_slots, row_bytes * num_slots);
+  const int spw = fused_samples(num_slots, row_bytes * num_slots, lanes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == CTI_EBAG_F32)
@@ -1836,36 +1839,9 @@ extern "C" int cti_ebag_forward(const void* values, int32_t index_type, int64_t 
 }
 
 namespace cti {
-namespace {
 
-// Rows per bag of a tile -> its bucket (0 = most rows per bag), as order_next computes it.
-inline int order_bucket(int64_t rows, int nb) {
-  int64_t per_bag = rows >= 0 ? rows >> __builtin_ctz(static_cast<unsigned>(nb)) : 0;  // nb is a power of two
-  per_bag = per_bag < 0 ? 0 : (per_bag > kOrderBuckets - 1 ? kOrderBuckets - 1 : per_bag);
-  return kOrderBuckets - 1 - static_cast<int>(per_bag);
-}
-
-inline int64_t host_offset(const void* a, int32_t type, int64_t i) {
-  return type == CTI_EBAG_I32 ? static_cast<int64_t>(static_cast<const int32_t*>(a)[i])
-                              : static_cast<const int64_t*>(a)[i];
-}
-
-}  // namespace
-}  // namespace cti
-
-extern "C" int cti_ebag_order_host(const void* row_offsets, int32_t offset_type, int64_t batch_size, int32_t num_slots,
-                                   int32_t table_dtype, int32_t emb_dim, int32_t* order, int64_t order_bytes) {
-  clear_error();
-  if (offset_type != CTI_EBAG_I64 && offset_type != CTI_EBAG_I32)
-    return set_error(CTI_EBAG_EINVAL, "unknown offset type code %d", offset_type);
-  if (!dtype_ok(table_dtype) && table_dtype != CTI_EBAG_I8)
-    return set_error(CTI_EBAG_EINVAL, "unknown table dtype code %d", table_dtype);
-  if (batch_size < 1 || num_slots < 1 || emb_dim < 1)
-    return set_error(CTI_EBAG_EINVAL, "batch_size, num_slots and emb_dim must be >= 1");
-  if (!row_offsets || !order) return set_error(CTI_EBAG_EINVAL, "NULL host pointer among row_offsets/order");
-  if (num_slots > kMaxFields)
-    return set_error(CTI_EBAG_EUNSUPPORTED, "a dispatch order covers at most %d slots (got %d)", kMaxFields, num_slots);
-  // the row shape the reference-layout launch takes for aligned buffers
+int order_bags_per_tile(int32_t table_dtype, int32_t emb_dim) {
+  // the row shape a launch takes for aligned buffers
   cti_ebag_table t;
   memset(&t, 0, sizeof(t));
   t.data = reinterpret_cast<const void*>(uintptr_t{256});
@@ -1874,63 +1850,10 @@ extern "C" int cti_ebag_order_host(const void* row_offsets, int32_t offset_type,
   t.dim = emb_dim;
   const int variant = pick_variant(t, dtype_bytes(table_dtype), 4, reinterpret_cast<void*>(uintptr_t{256}),
                                    static_cast<int64_t>(emb_dim) * 4);
-  if (variant == kVarGeneric)
-    return set_error(CTI_EBAG_EUNSUPPORTED, "rows of %d elements of this type take the element-wise kernel, which "
-                     "follows no order", emb_dim);
-  const int nb = bags_per_tile(variant);
-  const int64_t per_field = (batch_size + nb - 1) / nb;
-  const int64_t n = per_field * num_slots;
-  if (n > INT32_MAX / 2) return set_error(CTI_EBAG_EUNSUPPORTED, "batch of %lld samples has too many tiles", (long long)batch_size);
-  if (order_bytes < (kOrderHeader + n) * 4)
-    return set_error(CTI_EBAG_EINVAL, "order buffer of %lld bytes; this batch needs %lld", (long long)order_bytes,
-                     (long long)((kOrderHeader + n) * 4));
-  // Per XCD range (the tiles xcd_contiguous() gives one XCD) and per chunk of kOrderChunk tiles: a
-  // stable counting sort by bucket, as the device's order_next makes it (whose order inside a
-  // bucket is arbitrary).
-  const int64_t q = n >> 3, r = n & 7;
-  std::vector<unsigned char> bucket(kOrderChunk);
-  for (int x = 0; x < 8; ++x) {
-    const int64_t lo = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
-    const int64_t cnt = q + (x < r ? 1 : 0);
-    for (int64_t c0 = 0; c0 < cnt; c0 += kOrderChunk) {
-      const int64_t m = cnt - c0 < kOrderChunk ? cnt - c0 : kOrderChunk;
-      // four interleaved counts, so that runs of tiles in one bucket do not form one chain of
-      // dependent increments
-      int32_t cnt4[4][kOrderBuckets] = {};
-      // tiles of a chunk are consecutive: walk (field, tile in field) instead of dividing per tile
-      int64_t fi = (lo + c0) / per_field, local = lo + c0 - fi * per_field;
-      for (int64_t k = 0; k < m; ++k) {
-        const int64_t b0 = local * nb;
-        const int64_t b1 = b0 + nb < batch_size ? b0 + nb : batch_size;
-        const int64_t base = fi * (batch_size + 1);
-        const int bk = order_bucket(host_offset(row_offsets, offset_type, base + b1) -
-                                        host_offset(row_offsets, offset_type, base + b0), nb);
-        bucket[k] = static_cast<unsigned char>(bk);
-        ++cnt4[k & 3][bk];
-        if (++local == per_field) {
-          local = 0;
-          ++fi;
-        }
-      }
-      // stable placement: bucket b's tiles from lane 0, then 1, 2, 3 of each group of four would
-      // not be in tile order, so take the exclusive prefix over buckets and place in tile order
-      int32_t next[kOrderBuckets];
-      int32_t run = 0;
-      for (int b = 0; b < kOrderBuckets; ++b) {
-        next[b] = run;
-        run += cnt4[0][b] + cnt4[1][b] + cnt4[2][b] + cnt4[3][b];
-      }
-      int32_t* const dst = order + kOrderHeader + lo + c0;
-      const int32_t t0 = static_cast<int32_t>(lo + c0);
-      for (int64_t k = 0; k < m; ++k) dst[next[bucket[k]]++] = t0 + static_cast<int32_t>(k);
-    }
-  }
-  order[0] = static_cast<int32_t>(n);
-  order[1] = kOrderMagic;
-  order[2] = 0;
-  order[3] = 0;
-  return CTI_EBAG_OK;
+  return variant == kVarGeneric ? 0 : bags_per_tile(variant);
 }
+
+}  // namespace cti
 
 extern "C" int cti_ebag_fused_all_slots_ordered(const void* values, int32_t index_type, const void* val_offsets,
                                                 const void* row_offsets, int32_t offset_type, const void* weight,

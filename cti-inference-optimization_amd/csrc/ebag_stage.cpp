@@ -58,9 +58,13 @@ void convert_range(const void* src, int st, void* dst, int dt, int64_t b, int64_
   }
 }
 
-// One conversion job: up to kMaxParts arrays, each cut into chunks of at most `chunk` elements.
+// One job of the pool: either a conversion of up to kMaxParts arrays, each cut into chunks of at
+// most `chunk` elements, or `tasks` calls of task(ctx, i).
 constexpr int kMaxParts = 8;
 struct Job {
+  void (*task)(const void* ctx, int64_t i) = nullptr;
+  const void* ctx = nullptr;
+  int64_t tasks = 0;
   int parts = 0;
   const void* src[kMaxParts];
   int st[kMaxParts];
@@ -70,8 +74,12 @@ struct Job {
   int64_t first_chunk[kMaxParts + 1];  // prefix of per-part chunk counts
   int64_t chunk = 1;
 
-  int64_t chunks() const { return first_chunk[parts]; }
+  int64_t chunks() const { return task ? tasks : first_chunk[parts]; }
   void run_chunk(int64_t c) const {
+    if (task) {
+      task(ctx, c);
+      return;
+    }
     int p = 0;
     while (c >= first_chunk[p + 1]) ++p;
     const int64_t b = (c - first_chunk[p]) * chunk;
@@ -211,10 +219,140 @@ void run_job(Job& job, int64_t elements, int num_threads) {
   Pool::get().run(job, static_cast<int>(t - 1));
 }
 
+// ---------------------------------------------------------------------------------------------
+// Dispatch order made on the host (the layout is the one the pooling launch's own order pass
+// writes): each XCD's contiguous range of tile positions, in chunks of kOrderChunk tiles, holds
+// the chunk's tiles by rows per bag, most first (a stable counting sort). Chunks are independent
+// tasks for the pool.
+struct OrderJob {
+  const void* offsets;
+  int32_t offset_type;
+  int64_t stride;     // offsets between consecutive fields' first bags (B or B + 1)
+  int64_t batch;
+  int64_t per_field;  // tiles per field
+  int64_t n;          // tiles
+  int nb_log2;        // bags per tile (a power of two)
+  int32_t* order;
+  int64_t chunks_per_range;
+};
+
+template <typename OT>
+void order_chunk_typed(const OrderJob& j, int64_t lo, int64_t c0, int64_t m) {
+  const OT* const off = static_cast<const OT*>(j.offsets);
+  const int64_t nb = int64_t{1} << j.nb_log2;
+  unsigned char bucket[kOrderChunk];
+  // four interleaved counts, so that runs of tiles in one bucket do not form one chain of
+  // dependent increments
+  int32_t count[4][kOrderBuckets] = {};
+  // tiles of a chunk are consecutive: take them field by field, each field's run of tiles a plain
+  // strided walk over its offsets
+  int64_t fi = (lo + c0) / j.per_field, local = lo + c0 - fi * j.per_field;
+  for (int64_t k = 0; k < m;) {
+    const OT* const f_off = off + fi * j.stride;
+    const int64_t run = std::min<int64_t>(m - k, j.per_field - local);
+    // every tile of the run but the field's last spans nb full bags
+    const int64_t full = local + run < j.per_field ? run : run - 1;
+    for (int64_t t = 0; t < full; ++t) {
+      const int64_t b0 = (local + t) << j.nb_log2;
+      const int64_t rows = static_cast<int64_t>(f_off[b0 + nb]) - static_cast<int64_t>(f_off[b0]);
+      int64_t per_bag = rows > 0 ? rows >> j.nb_log2 : 0;
+      per_bag = per_bag > kOrderBuckets - 1 ? kOrderBuckets - 1 : per_bag;
+      bucket[k + t] = static_cast<unsigned char>(kOrderBuckets - 1 - per_bag);
+    }
+    if (full < run) {  // the field's last tile ends at the batch's last bag
+      const int64_t b0 = (local + full) << j.nb_log2;
+      const int64_t rows = static_cast<int64_t>(f_off[j.batch]) - static_cast<int64_t>(f_off[b0]);
+      int64_t per_bag = rows > 0 ? rows >> j.nb_log2 : 0;
+      per_bag = per_bag > kOrderBuckets - 1 ? kOrderBuckets - 1 : per_bag;
+      bucket[k + full] = static_cast<unsigned char>(kOrderBuckets - 1 - per_bag);
+    }
+    k += run;
+    local = 0;
+    ++fi;
+  }
+  for (int64_t k = 0; k < m; ++k) ++count[k & 3][bucket[k]];
+  int32_t next[kOrderBuckets];
+  int32_t total = 0;
+  for (int b = 0; b < kOrderBuckets; ++b) {
+    next[b] = total;
+    total += count[0][b] + count[1][b] + count[2][b] + count[3][b];
+  }
+  int32_t* const dst = j.order + kOrderHeader + lo + c0;
+  const int32_t t0 = static_cast<int32_t>(lo + c0);
+  for (int64_t k = 0; k < m; ++k) dst[next[bucket[k]]++] = t0 + static_cast<int32_t>(k);
+}
+
+void order_chunk(const void* ctx, int64_t task) {
+  const OrderJob& j = *static_cast<const OrderJob*>(ctx);
+  const int64_t x = task / j.chunks_per_range, c0 = (task % j.chunks_per_range) * kOrderChunk;
+  const int64_t q = j.n >> 3, r = j.n & 7;
+  const int64_t lo = x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q;
+  const int64_t cnt = q + (x < r ? 1 : 0);
+  if (c0 >= cnt) return;
+  const int64_t m = cnt - c0 < kOrderChunk ? cnt - c0 : kOrderChunk;
+  if (j.offset_type == CTI_EBAG_I32) order_chunk_typed<int32_t>(j, lo, c0, m);
+  else order_chunk_typed<int64_t>(j, lo, c0, m);
+}
+
 }  // namespace
 }  // namespace cti
 
 using namespace cti;
+
+extern "C" int cti_ebag_order_host(const void* offsets, int32_t offset_type, int64_t offsets_stride,
+                                   int64_t batch_size, int32_t num_slots, int32_t table_dtype, int32_t emb_dim,
+                                   int32_t* order, int64_t order_bytes, int32_t num_threads) {
+  clear_error();
+  if (offset_type != CTI_EBAG_I64 && offset_type != CTI_EBAG_I32)
+    return set_error(CTI_EBAG_EINVAL, "unknown offset type code %d", offset_type);
+  if (dtype_bytes(table_dtype) == 0) return set_error(CTI_EBAG_EINVAL, "unknown table dtype code %d", table_dtype);
+  if (batch_size < 1 || num_slots < 1 || emb_dim < 1)
+    return set_error(CTI_EBAG_EINVAL, "batch_size, num_slots and emb_dim must be >= 1");
+  if (offsets_stride != batch_size && offsets_stride != batch_size + 1)
+    return set_error(CTI_EBAG_EINVAL, "offsets_stride must be batch_size (global offsets) or batch_size + 1 (slot "
+                     "row offsets), got %lld", (long long)offsets_stride);
+  if (!offsets || !order) return set_error(CTI_EBAG_EINVAL, "NULL host pointer among offsets/order");
+  if (num_threads < 1 || num_threads > 256)
+    return set_error(CTI_EBAG_EINVAL, "num_threads must be in [1, 256] (got %d)", num_threads);
+  if (num_slots > kOrderMaxFields)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "a dispatch order covers at most %d slots (got %d)", kOrderMaxFields,
+                     num_slots);
+  const int nb = order_bags_per_tile(table_dtype, emb_dim);
+  if (nb == 0)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "rows of %d elements of this type take the element-wise kernel, which "
+                     "follows no order", emb_dim);
+  OrderJob oj;
+  oj.offsets = offsets;
+  oj.offset_type = offset_type;
+  oj.stride = offsets_stride;
+  oj.batch = batch_size;
+  oj.per_field = (batch_size + nb - 1) / nb;
+  oj.n = oj.per_field * num_slots;
+  oj.nb_log2 = __builtin_ctz(static_cast<unsigned>(nb));
+  oj.order = order;
+  if (oj.n > INT32_MAX / 2)
+    return set_error(CTI_EBAG_EUNSUPPORTED, "batch of %lld samples has too many tiles", (long long)batch_size);
+  if (order_bytes < (kOrderHeader + oj.n) * 4)
+    return set_error(CTI_EBAG_EINVAL, "order buffer of %lld bytes; this batch needs %lld", (long long)order_bytes,
+                     (long long)((kOrderHeader + oj.n) * 4));
+  oj.chunks_per_range = ((oj.n + 7) / 8 + kOrderChunk - 1) / kOrderChunk;
+  Job job;
+  job.task = order_chunk;
+  job.ctx = &oj;
+  job.tasks = 8 * oj.chunks_per_range;
+  // one task per chunk of an XCD range; below ~2k tiles one thread is faster than waking others
+  const int threads = static_cast<int>(std::min<int64_t>(num_threads, std::max<int64_t>(1, oj.n / 2048)));
+  if (threads <= 1) {
+    for (int64_t t = 0; t < job.tasks; ++t) order_chunk(&oj, t);
+  } else {
+    Pool::get().run(job, std::min(threads, static_cast<int>(job.tasks)) - 1);
+  }
+  order[0] = static_cast<int32_t>(oj.n);
+  order[1] = kOrderMagic;
+  order[2] = 0;
+  order[3] = 0;
+  return CTI_EBAG_OK;
+}
 
 extern "C" int cti_ebag_narrow_ids(const int64_t* src, int64_t n, int32_t* dst, int32_t num_threads) {
   clear_error();

@@ -19,6 +19,7 @@ Both validate their arguments on the host (no device synchronisation) and raise 
 from __future__ import annotations
 
 import ctypes
+import os
 from typing import Optional, Sequence
 
 import torch
@@ -204,30 +205,41 @@ def order_bytes(batch_size: int, num_slots: int) -> int:
     return n
 
 
-def make_tile_order(flat_row_offsets: torch.Tensor, batch_size: int, num_slots: int, table_dtype: torch.dtype,
-                    emb_dim: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """The dispatch order of the reference-layout launch for this batch, made on the host from its
-    row offsets (a CPU int64 / int32 tensor ``[num_slots*(B+1)]``): each XCD's tiles, most rows per
-    bag first. ``table_dtype`` / ``emb_dim`` are the table's (int8 tables: ``torch.int8``). Returns
-    a CPU int32 tensor (``out`` if given, of at least ``order_bytes(B, S)`` bytes) to be moved to
-    the device with the batch and passed as ``tile_order``. No counterpart in the reference."""
-    if flat_row_offsets.device.type != "cpu" or flat_row_offsets.dtype not in (torch.int64, torch.int32):
-        raise ValueError("flat_row_offsets must be an int64 or int32 CPU tensor")
-    flat_row_offsets = flat_row_offsets.contiguous()
+def make_tile_order(offsets: torch.Tensor, batch_size: int, num_slots: int, table_dtype: torch.dtype,
+                    emb_dim: int, out: Optional[torch.Tensor] = None, threads: int = 0) -> torch.Tensor:
+    """The dispatch order of the launch for this batch, made on the host from its offsets (a CPU
+    int64 / int32 tensor): the reference layout's row offsets ``[num_slots*(B+1)]`` or the global
+    offsets ``[num_slots*B+1]`` of ``embedding_bag_pooled`` / ``PooledEmbedding``. Each XCD's
+    tiles are listed most rows per bag first. ``table_dtype`` / ``emb_dim`` are the rows' (one
+    width for all slots; int8 tables: ``torch.int8``). Returns a CPU int32 tensor (``out`` if
+    given, of at least ``order_bytes(B, S)`` bytes) to be moved to the device with the batch and
+    passed as ``tile_order``. ``threads``: host threads (0: up to 16, within this host's CPUs).
+    No counterpart in the reference."""
+    if offsets.device.type != "cpu" or offsets.dtype not in (torch.int64, torch.int32):
+        raise ValueError("offsets must be an int64 or int32 CPU tensor")
+    offsets = offsets.contiguous()
     batch_size, num_slots = int(batch_size), int(num_slots)
-    if flat_row_offsets.numel() != num_slots * (batch_size + 1):
-        raise ValueError(f"flat_row_offsets has {flat_row_offsets.numel()} entries, expected "
-                         f"{num_slots} * ({batch_size} + 1)")
+    if offsets.numel() == num_slots * (batch_size + 1):
+        stride = batch_size + 1
+    elif offsets.numel() == num_slots * batch_size + 1:
+        stride = batch_size
+    else:
+        raise ValueError(f"offsets has {offsets.numel()} entries, expected {num_slots} * ({batch_size} + 1) (slot "
+                         f"row offsets) or {num_slots} * {batch_size} + 1 (global offsets)")
     nbytes = order_bytes(batch_size, num_slots)
     if out is None:
         out = torch.empty((nbytes + 3) // 4, dtype=torch.int32)
     elif out.device.type != "cpu" or out.dtype != torch.int32 or not out.is_contiguous() or out.numel() * 4 < nbytes:
         raise ValueError(f"out must be a contiguous CPU int32 tensor of at least {nbytes} bytes")
     tcode = _capi.I8 if table_dtype == torch.int8 else _capi.dtype_code(table_dtype)
-    _capi.check(_capi.lib().cti_ebag_order_host(flat_row_offsets.data_ptr(), _capi.index_code(flat_row_offsets.dtype),
+    _capi.check(_capi.lib().cti_ebag_order_host(offsets.data_ptr(), _capi.index_code(offsets.dtype), stride,
                                                 batch_size, num_slots, tcode, int(emb_dim), out.data_ptr(),
-                                                out.numel() * 4))
+                                                out.numel() * 4, int(threads) or _host_threads()))
     return out
+
+
+def _host_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
 
 
 def fused_all_slots_embedding(
@@ -489,7 +501,11 @@ class PooledEmbedding:
     With ``use_bins`` the plan owns one workspace, sized for ``max_batch`` samples, whose list
     counter every call leaves at zero (calls on one plan must not overlap).
 
-    With ``dispatch_order`` a serving loop passes the next batch's offsets with each call
+    A call may follow an order made on the host from the batch's offsets where the batch is
+    produced (``plan(values, offsets, out, tile_order=make_tile_order(...).to(device))``): each
+    XCD starts its tiles with the most rows per bag, which shortens the launch's drain; the output
+    is the same bit for bit. With ``dispatch_order`` instead, a serving loop that holds no host
+    offsets passes the next batch's device offsets with each call
     (``plan(values, offsets, out, next_offsets=...)``): the launch also sorts that batch's tiles,
     most rows per bag first within each XCD's share, and the next call follows that order, which
     shortens the drain at the end of its launch. The plan alternates two device order buffers;
@@ -536,7 +552,7 @@ class PooledEmbedding:
         return self._orders
 
     def __call__(self, values: torch.Tensor, offsets: torch.Tensor, out: Optional[torch.Tensor] = None,
-                 next_offsets: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 next_offsets: Optional[torch.Tensor] = None, tile_order: Optional[torch.Tensor] = None) -> torch.Tensor:
         if values.device != self.device or offsets.device != self.device:
             raise ValueError(f"values and offsets must be on {self.device}")
         if offsets.dtype != torch.int64 or not offsets.is_contiguous() or not values.is_contiguous():
@@ -560,6 +576,18 @@ class PooledEmbedding:
                 raise ValueError(f"next_offsets must be contiguous int64 with {n_off} entries on {self.device}")
         stream = torch.cuda.current_stream(self.device).cuda_stream
         opts = self._opts  # read by the C call before it returns
+        if tile_order is not None:
+            if self.dispatch_order:
+                raise ValueError("tile_order (an order made on the host) and dispatch_order=True (orders made one "
+                                 "launch ahead) do not combine")
+            if tile_order.device != self.device or tile_order.dtype != torch.int32 or not tile_order.is_contiguous():
+                raise ValueError(f"tile_order must be a contiguous int32 tensor on {self.device}")
+            opts.tile_order = tile_order.data_ptr()
+            opts.next_order = opts.next_offsets = None
+            opts.order_bytes = tile_order.numel() * 4
+        elif not self.dispatch_order:
+            opts.tile_order = opts.next_order = opts.next_offsets = None
+            opts.order_bytes = 0
         if self.dispatch_order:
             orders = self._order_buffers(batch)
             opts.tile_order = orders[self._cur].data_ptr() if self._have_order else None

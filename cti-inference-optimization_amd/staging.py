@@ -125,7 +125,7 @@ class InputStager:
             from .ops import make_tile_order, order_bytes
             batch_size = n_off // self.num_slots - 1
             make_tile_order(ts[1], batch_size, self.num_slots, self.order_for[0], self.order_for[1],
-                            out=self._order_host)
+                            out=self._order_host, threads=self.threads)
             ts = ts + [self._order_host[:(order_bytes(batch_size, self.num_slots) + 3) // 4]]
             counts.append(ts[3].numel())
         n = len(ts)

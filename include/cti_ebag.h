@@ -288,21 +288,27 @@ int cti_ebag_fused_all_slots_typed(const void* values, int32_t index_type, const
                                    int64_t nnz, void* stream);
 
 /*
- * Dispatch order of a reference-layout launch, made on the HOST where the batch's offsets are
- * produced (no counterpart in the reference). The reference's Triton launch runs one program per
- * bag (online_best/infer.py:1053); here a launch ends with a drain when tiles of long bags start
+ * Dispatch order of a launch, made on the HOST where the batch's offsets are produced (no
+ * counterpart in the reference). The reference's Triton launch runs one program per bag
+ * (online_best/infer.py:1053); here a launch ends with a drain when tiles of long bags start
  * late. An order lists each XCD's tiles most rows per bag first, which removes most of it; a
  * collate or staging pass that already holds the offsets makes it at no cost to the GPU, and the
- * launch then follows it (cti_ebag_fused_all_slots_ordered). Results are the same bit for bit
- * with or without an order, and with an order made for another batch.
- *   row_offsets  HOST [num_slots*(B+1)] of `offset_type` (I64 / I32), as the launch will read
- *   table_dtype, emb_dim   the launch's table (they fix how many bags a tile holds)
- *   order        HOST int32 buffer of order_bytes >= cti_ebag_order_bytes(batch_size, num_slots)
+ * launch then follows it (cti_ebag_fused_all_slots_ordered; cti_ebag_forward with
+ * opts->tile_order). Results are the same bit for bit with or without an order, and with an
+ * order made for another batch.
+ *   offsets         HOST offsets as the launch will read them, of `offset_type` (I64 / I32):
+ *                   the reference layout's row_offsets [num_slots*(B+1)] (offsets_stride = B+1)
+ *                   or the global offsets [num_slots*B+1] of cti_ebag_forward (offsets_stride = B)
+ *   table_dtype, emb_dim   the launch's rows, one width for every slot (they fix how many bags a
+ *                   tile holds)
+ *   order           HOST int32 buffer of order_bytes >= cti_ebag_order_bytes(batch_size, num_slots)
+ *   num_threads     host threads to use (1..256; the staging calls' persistent pool)
  * CTI_EBAG_EUNSUPPORTED for rows that take the element-wise kernel (not whole 16-byte vectors,
- * or wider than 4 KB) and for more than 64 slots.
+ * or wider than 4 KB) and for more than 64 slots. Synchronous.
  */
-int cti_ebag_order_host(const void* row_offsets, int32_t offset_type, int64_t batch_size, int32_t num_slots,
-                        int32_t table_dtype, int32_t emb_dim, int32_t* order, int64_t order_bytes);
+int cti_ebag_order_host(const void* offsets, int32_t offset_type, int64_t offsets_stride, int64_t batch_size,
+                        int32_t num_slots, int32_t table_dtype, int32_t emb_dim, int32_t* order,
+                        int64_t order_bytes, int32_t num_threads);
 
 /*
  * cti_ebag_fused_all_slots_typed following a dispatch order (NULL = none): `tile_order` is a

@@ -19,7 +19,9 @@ def bench():
 
 
 @pytest.mark.parametrize("workload,kernel", [("bf16-2m", "pool_kernel"), ("bf16-2m-int8", "pool_kernel"),
-                                             ("lazy-32k", "pool_kernel"), ("hetero-bf16", "bin_mixed_long_kernels")])
+                                             ("lazy-32k", "pool_kernel"), ("hetero-bf16", "bin_mixed_long_kernels"),
+                                             ("reference-5m", "pool_kernel"), ("reference-5m", "pool_norm_kernel"),
+                                             ("reference-5m-int8", "pool_kernel")])
 def test_profiles_give_the_traffic(bench, workload, kernel):
     # every profile the bench line cites exists and carries its measured HBM bytes per launch,
     # which sit between the output bytes written and 4 GB

@@ -418,6 +418,11 @@ def test_host_order_is_a_sorted_permutation(pkg, dt, D, nb, S, B):
     tpf = (B + nb - 1) // nb
     n = S * tpf
     assert np.array_equal(o[:4 + n], b.numpy()[:4 + n])  # entries past the order are not written
+    # the same bags in the global layout (offsets[f*B + b], one closing entry) give the same order
+    base = np.concatenate([[0], np.cumsum(ro[:, -1])[:-1]])
+    glob = np.concatenate([(ro[:, :-1] + base[:, None]).reshape(-1), [base[-1] + ro[-1, -1]]]).astype(np.int64)
+    g = pkg.make_tile_order(torch.from_numpy(glob), B, S, dt, D)
+    assert np.array_equal(o[:4 + n], g.numpy()[:4 + n])
     assert o[0] == n and o[1] == 0x4F524452 and o[2] == 0 and o[3] == 0
     perm = o[4:4 + n]
     q, r = n >> 3, n & 7
@@ -444,13 +449,16 @@ def test_host_order_rejections(pkg):
     ro = torch.zeros(3 * 11, dtype=torch.int64)
     buf = torch.zeros(64, dtype=torch.int32)
     call = lambda *a: lib.cti_ebag_order_host(*a)  # noqa: E731
-    assert call(ro.data_ptr(), c.I64, 10, 3, c.BF16, 128, buf.data_ptr(), 36) == c.EINVAL  # 6 tiles need 40 bytes
-    assert call(ro.data_ptr(), c.I64, 10, 3, c.BF16, 128, buf.data_ptr(), 40) == c.OK
-    assert call(ro.data_ptr(), c.I64, 10, 3, c.BF16, 100, buf.data_ptr(), 1 << 20) == c.EUNSUPPORTED  # element-wise
-    assert call(ro.data_ptr(), 7, 10, 3, c.BF16, 128, buf.data_ptr(), 1 << 20) == c.EINVAL
-    assert call(None, c.I64, 10, 3, c.BF16, 128, buf.data_ptr(), 1 << 20) == c.EINVAL
-    assert call(ro.data_ptr(), c.I64, 0, 3, c.BF16, 128, buf.data_ptr(), 1 << 20) == c.EINVAL
+    assert call(ro.data_ptr(), c.I64, 11, 10, 3, c.BF16, 128, buf.data_ptr(), 36, 1) == c.EINVAL  # 6 tiles need 40 B
+    assert call(ro.data_ptr(), c.I64, 11, 10, 3, c.BF16, 128, buf.data_ptr(), 40, 1) == c.OK
+    assert call(ro.data_ptr(), c.I64, 10, 10, 3, c.BF16, 128, buf.data_ptr(), 40, 1) == c.OK  # global offsets
+    assert call(ro.data_ptr(), c.I64, 12, 10, 3, c.BF16, 128, buf.data_ptr(), 40, 1) == c.EINVAL  # stride
+    assert call(ro.data_ptr(), c.I64, 11, 10, 3, c.BF16, 100, buf.data_ptr(), 1 << 20, 1) == c.EUNSUPPORTED  # generic
+    assert call(ro.data_ptr(), 7, 11, 10, 3, c.BF16, 128, buf.data_ptr(), 1 << 20, 1) == c.EINVAL
+    assert call(None, c.I64, 11, 10, 3, c.BF16, 128, buf.data_ptr(), 1 << 20, 1) == c.EINVAL
+    assert call(ro.data_ptr(), c.I64, 1, 0, 3, c.BF16, 128, buf.data_ptr(), 1 << 20, 1) == c.EINVAL
+    assert call(ro.data_ptr(), c.I64, 11, 10, 3, c.BF16, 128, buf.data_ptr(), 40, 0) == c.EINVAL  # threads
     big = torch.zeros(65 * 11, dtype=torch.int64)
-    assert call(big.data_ptr(), c.I64, 10, 65, c.BF16, 128, buf.data_ptr(), 1 << 20) == c.EUNSUPPORTED
+    assert call(big.data_ptr(), c.I64, 11, 10, 65, c.BF16, 128, buf.data_ptr(), 1 << 20, 1) == c.EUNSUPPORTED
     with pytest.raises(ValueError):
         pkg.make_tile_order(torch.zeros(7, dtype=torch.int64), 10, 3, torch.bfloat16, 128)

@@ -334,3 +334,38 @@ def test_stager_with_orders_matches_oracle(pkg, dev):
         want = orc.pool_c(h["_flat_values"].numpy(), h["_flat_row_offsets"].numpy(), [table] * S, "bf16", "sum",
                           batch=B, val_base=h["_val_offsets"].numpy())
         assert np.array_equal(to_np(got, "bf16"), want)
+
+
+@pytest.mark.parametrize("shape", range(len(HOST_SHAPES)))
+def test_plan_follows_host_order_global_layout(pkg, dev, shape):
+    """PooledEmbedding(...)(values, offsets, tile_order=...) with an order made on the host from
+    the global offsets equals the plain call bit for bit (own batch, another batch's order,
+    another batch size's order in a large enough buffer), per-field tables, sum and mean."""
+    tdt, D, S, B, max_len = HOST_SHAPES[shape]
+    print(f"plan host order: {tdt} D={D} S={S} B={B}", flush=True)
+    rng = np.random.default_rng(300 + shape)
+    tables = [to_dev(make_table(rng, V, D, tdt), tdt, dev) for _ in range(S)]
+    tdt_t = {"bf16": torch.bfloat16, "f32": torch.float32}[tdt]
+    for pooling in ("sum", "mean"):
+        plan = pkg.PooledEmbedding(tables, pooling=pooling)
+        offs = []
+        for k in range(3):
+            L = rng.integers(0, max_len + 1, size=(S, B))
+            if k == 1:
+                L[:, ::5] = rng.integers(100, 250, size=L[:, ::5].shape)
+            o = np.zeros(S * B + 1, np.int64)
+            np.cumsum(L.reshape(-1), out=o[1:])
+            offs.append(o)
+        for k, o in enumerate(offs):
+            v = torch.from_numpy(make_ids(rng, int(o[-1]), V)).to(dev)
+            do = torch.from_numpy(o).to(dev)
+            plain = plan(v, do)
+            small_o = offs[(k + 2) % 3][:S * max(1, B // 4) + 1].copy()
+            orders = [pkg.make_tile_order(torch.from_numpy(o), B, S, tdt_t, D),
+                      pkg.make_tile_order(torch.from_numpy(offs[(k + 1) % 3]), B, S, tdt_t, D),
+                      pkg.make_tile_order(torch.from_numpy(small_o), max(1, B // 4), S, tdt_t, D,
+                                          out=torch.zeros(pkg.order_bytes(B, S) // 4, dtype=torch.int32))]
+            for order in orders:
+                got = plan(v, do, tile_order=order.to(dev))
+                torch.cuda.synchronize()
+                assert torch.equal(_bits(got), _bits(plain)), pooling
