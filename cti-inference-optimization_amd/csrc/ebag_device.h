@@ -273,6 +273,34 @@ __device__ __forceinline__ float block_sum(float v, float* s_red) {
   }
 }
 
+// N sums over the workgroup at once (each as block_sum would take it: the same butterfly and
+// wavefront order, so each result is bitwise what block_sum<WAVES> gives), two barriers in all.
+// s_red holds WAVES * N floats.
+template <int WAVES, int N>
+__device__ __forceinline__ void block_sum_n(float* v, float* s_red) {
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v[k] += shfl_xor_f32(v[k], m);
+  }
+  if constexpr (WAVES > 1) {
+    const int w = static_cast<int>(threadIdx.x) / kWave;
+    __syncthreads();  // earlier readers of s_red are done
+    if (lane_id() == 0) {
+#pragma unroll
+      for (int k = 0; k < N; ++k) s_red[k * WAVES + w] = v[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < WAVES; ++i) t += s_red[k * WAVES + i];
+      v[k] = t;
+    }
+  }
+}
+
 __device__ __forceinline__ void unpack16(const uint4& v, float* a, float) {
   a[0] = __uint_as_float(v.x);
   a[1] = __uint_as_float(v.y);

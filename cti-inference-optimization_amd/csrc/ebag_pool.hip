@@ -657,12 +657,13 @@ __global__ void __launch_bounds__(kMainThreads) pool_mixed_kernel(const PoolPara
 // Pooling with the input LayerNorm fused into the writer (online_best/infer.py:1050-1076): one
 // workgroup owns whole output rows, so the pooled row never goes to HBM before normalisation.
 // One shared table (the reference's single nn.Embedding), uniform row width, one row vector per
-// lane. Wavefront w pools fields w, w + W, ... of its sample exactly as the main kernel pools a
+// lane. The workgroup's bags (its samples x all fields) are dealt to its W wavefronts by length,
+// so that each gets a like share; a wavefront pools its bags exactly as the main kernel pools a
 // tile (length-ranked rounds, one lane group per short bag in element order, the whole
 // wavefront for longer bags) and writes each result, rounded to the output type, into an LDS
-// copy of the row; the workgroup then normalises that row (fp32 mean and variance, fixed
-// reduction order) and stores it once.
-constexpr int kFusedBagsPerWave = 32;  // samples per workgroup * ceil(fields / waves) <= 32
+// copy of the rows; the workgroup then normalises the rows (fp32 mean and variance, fixed
+// reduction order) and stores each once.
+constexpr int kFusedBags = kWave;  // samples per workgroup * fields <= 64: one lane per bag
 
 // Wavefronts per fused workgroup for rows of `lanes` lanes (one 16-byte vector per lane).
 // Measured (reference shape: 28 slots of 1 KiB rows, B = 4096; bf16-2m shape: 256-byte rows):
@@ -671,9 +672,9 @@ constexpr int fused_waves(int lanes) { return lanes >= 64 ? 8 : 4; }
 
 struct FusedLds {  // one per wavefront
   unsigned int ids[kWave];
-  int order[kFusedBagsPerWave];
-  int len[kFusedBagsPerWave];
-  int64_t start[kFusedBagsPerWave];
+  int order[kFusedBags / 4];  // this wavefront's short bags in list order (at most 64 / 4 per wavefront)
+  int len[kFusedBags];
+  int64_t start[kFusedBags];
 };
 
 struct FusedNorm {
@@ -691,9 +692,10 @@ __global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p
   using S = Shape<TT, LANES, 1>;
   constexpr int U = S::U;
   constexpr int R = S::R;
+  static_assert(W >= 4, "a wavefront's list of short bags holds at most kFusedBags / 4 entries");
   extern __shared__ uint4 s_row_raw[];  // the output rows: SPW * F * D elements of TT
   __shared__ FusedLds s_w[W];
-  __shared__ float s_red[W];
+  __shared__ float s_red[W * SPW];
   TT* const row = reinterpret_cast<TT*>(s_row_raw);
 
   const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -710,30 +712,40 @@ __global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p
   const unsigned int r_pad = BUF ? 0xffffffffu >> shift : 0u;
   FusedLds& s = s_w[wave];
 
-  // Lane i describes this wavefront's bag i: field wave + W * (i % nk) of sample b0 + i / nk.
-  // Row position of bag i in the LDS rows: (i / nk) * F + field.
-  const int nk = wave < F ? (F - wave + W - 1) / W : 0;
-  auto bag_pos = [&](int i) { return (i / nk) * F + wave + W * (i % nk); };
-  bool valid = lane < SPW * nk;
+  // Every wavefront describes all SPW * F bags of the workgroup, bag i on lane i (sample b0 + i / F,
+  // field i % F; its pooled row goes to LDS row position i), ranks them by length (longest first,
+  // ties by position) and keeps the ranks dealt to it: rank r goes to wavefront r % W when r / W
+  // is even, W - 1 - r % W when odd, at position r / W of that wavefront's list. So each wavefront
+  // gets a like share of the long and of the short bags and the workgroup's slowest wavefront (the
+  // one the LayerNorm waits for) has about the average load. Each bag is pooled exactly as before
+  // (one lane group in element order, or the whole wavefront above sub_threshold), so the pooled
+  // rows do not depend on who pools them. Bags above sub_threshold have the first ranks, so they
+  // come first in every list.
+  const int nb = SPW * F;  // <= kFusedBags (host)
+  bool valid = lane < nb;
   int64_t start = 0, end = 0;
   if (valid) {
-    const int64_t bb = b0 + lane / nk;
+    const int64_t bb = b0 + lane / F;
     valid = bb < p.batch;
-    if (valid) bag_range(p, p.f[wave + W * (lane % nk)].gidx, bb, start, end);
+    if (valid) bag_range(p, p.f[lane % F].gidx, bb, start, end);
   }
   const int64_t L = end - start;
-  const bool shortb = valid && L <= p.sub_threshold;
-  const bool medium = valid && L > p.sub_threshold;
-  const int n_short = __popcll(__ballot(shortb));
-  const int key = shortb ? static_cast<int>(L) : -1;
+  const int key = valid ? static_cast<int>(L < INT32_MAX ? L : INT32_MAX) : -1;
   int rank = 0;
-#pragma unroll
-  for (int j = 0; j < kFusedBagsPerWave; ++j) {
+  // unrolled by 8 only: each unrolled readlane holds a scalar register
+#pragma unroll 8
+  for (int j = 0; j < kFusedBags; ++j) {
     const int kj = __builtin_amdgcn_readlane(key, j);
     rank += (kj > key || (kj == key && j < lane)) ? 1 : 0;
   }
+  const int rd = rank / W, rm = rank - rd * W;
+  const bool mine = valid && ((rd & 1) ? W - 1 - rm : rm) == wave;
+  const bool medium = mine && L > p.sub_threshold;
+  const bool shortb = mine && L <= p.sub_threshold;
+  const int n_medium = __popcll(__ballot(medium));
+  const int n_short = __popcll(__ballot(shortb));
   if (shortb) {
-    s.order[rank] = lane;
+    s.order[rd - n_medium] = lane;
     s.len[lane] = static_cast<int>(L);
     s.start[lane] = start;
   }
@@ -745,7 +757,7 @@ __global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p
     for (int i = 0; i < S::NACC; ++i) r[i] = a[i];
     if (p.pooling == CTI_EBAG_MEAN && Lb > 0)
       div_by_count<S::NACC>(r, 1.0 / static_cast<double>(Lb), static_cast<float>(Lb));
-    store_out<S::VEC>(row + static_cast<int64_t>(bag_pos(bag)) * D + sl * S::VEC, r);
+    store_out<S::VEC>(row + static_cast<int64_t>(bag) * D + sl * S::VEC, r);
   };
 
   for (int r0 = 0; r0 < n_short; r0 += R) {
@@ -811,6 +823,8 @@ __global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p
   const char* const rb = reinterpret_cast<const char*>(row);
   const int64_t rstride = static_cast<int64_t>(cols) * Elem<TT>::kBytes;
   const float n = static_cast<float>(cols);
+  // the SPW rows' sums share one workgroup reduction, then their squared deviations share one
+  // (taking the sums while the rows are written held 4 more VGPRs: 7 wavefronts per SIMD)
   float mean[SPW], rstd[SPW];
 #pragma unroll
   for (int j = 0; j < SPW; ++j) {
@@ -821,7 +835,12 @@ __global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p
 #pragma unroll
       for (int e = 0; e < VEC; ++e) sum += x[e];
     }
-    mean[j] = block_sum<W>(sum, s_red) / n;
+    mean[j] = sum;
+  }
+  block_sum_n<W, SPW>(mean, s_red);
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    mean[j] /= n;
     float q = 0.f;
     for (int i = t; i < nvec; i += THREADS) {
       float x[VEC];
@@ -832,8 +851,11 @@ __global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p
         q += d * d;
       }
     }
-    rstd[j] = 1.0f / __builtin_sqrtf(block_sum<W>(q, s_red) / n + fn.eps);
+    rstd[j] = q;
   }
+  block_sum_n<W, SPW>(rstd, s_red);
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) rstd[j] = 1.0f / __builtin_sqrtf(rstd[j] / n + fn.eps);
   for (int i = t; i < nvec; i += THREADS) {
     float gm[VEC], bt[VEC];
     load_params<PT, VEC>(fn.gamma, static_cast<int64_t>(i) * VEC, gm);
@@ -1614,14 +1636,12 @@ hipError_t launch_fused_lanes(int lanes, const PoolParams& p, const FusedNorm& f
 
 constexpr int kFusedSamples = 2;  // measured: 1 / 2 / 4 samples per workgroup 45.7 / 40.5 / 44.6 us
 
-// Samples per fused workgroup: up to kFusedSamples, while every wavefront's bags fit
-// its lanes' bookkeeping and the LDS rows stay within kFusedLdsMax.
+// Samples per fused workgroup: up to kFusedSamples, while the workgroup's bags fit one lane each
+// and the LDS rows stay within kFusedLdsMax.
 constexpr int64_t kFusedLdsMax = 64 * 1024;
-int fused_samples(int num_slots, int64_t row_out_bytes, int lanes) {
-  const int waves = fused_waves(lanes);
-  const int per_wave = (num_slots + waves - 1) / waves;
+int fused_samples(int num_slots, int64_t row_out_bytes) {
   int spw = kFusedSamples;
-  while (spw > 1 && (spw * per_wave > kFusedBagsPerWave || spw * row_out_bytes > kFusedLdsMax / 2)) spw /= 2;
+  while (spw > 1 && (spw * num_slots > kFusedBags || spw * row_out_bytes > kFusedLdsMax / 2)) spw /= 2;
   return spw;
 }
 
@@ -1708,7 +1728,7 @@ extern "C" int cti_ebag_fused_all_slots_layernorm(const void* values, int32_t in
   fn.beta = beta;
   fn.eps = eps;
   const size_t row_lds = static_cast<size_t>(row_bytes * num_slots);
-  const int spw = fused_samples(num_slots, row_bytes * num_slots, lanes);
+  const int spw = fused_samples(num_slots, row_bytes * num_slots);
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == CTI_EBAG_F32)
