@@ -42,7 +42,9 @@ class InputStager:
     and offsets (else int64, as the reference sends them). ``order_for=(table dtype, emb_dim)``
     (with ``compact``) also makes each batch's dispatch order on the host from the offsets being
     staged and sends it in the same copy as ``_tile_order``, which ``fused_embedding`` and
-    ``RepEncoder`` follow (results unchanged bit for bit). Dropping the stager (or ``close()``)
+    ``RepEncoder`` follow (results unchanged bit for bit); a batch that already carries a host
+    ``_tile_order`` (made by its producer with ``make_tile_order``) has that one sent instead.
+    Dropping the stager (or ``close()``)
     waits for its copies; work that still reads a staged batch must be ordered before any reuse of
     that memory by the caller.
     """
@@ -124,9 +126,16 @@ class InputStager:
         if self.order_for is not None:
             from .ops import make_tile_order, order_bytes
             batch_size = n_off // self.num_slots - 1
-            make_tile_order(ts[1], batch_size, self.num_slots, self.order_for[0], self.order_for[1],
-                            out=self._order_host, threads=self.threads)
-            ts = ts + [self._order_host[:(order_bytes(batch_size, self.num_slots) + 3) // 4]]
+            n_order = (order_bytes(batch_size, self.num_slots) + 3) // 4
+            made = batch.get("_tile_order")
+            if made is not None:  # made by the batch's producer (e.g. its collate), shipped as it is
+                if made.device.type != "cpu" or made.dtype != torch.int32 or made.numel() > self._order_elems:
+                    raise ValueError(f"_tile_order must be a CPU int32 tensor of at most {self._order_elems} entries")
+                ts = ts + [made.contiguous()]
+            else:
+                make_tile_order(ts[1], batch_size, self.num_slots, self.order_for[0], self.order_for[1],
+                                out=self._order_host, threads=self.threads)
+                ts = ts + [self._order_host[:n_order]]
             counts.append(ts[3].numel())
         n = len(ts)
         src = (ctypes.c_void_p * n)(*[t.data_ptr() if t.numel() else None for t in ts])

@@ -321,12 +321,19 @@ def test_stager_with_orders_matches_oracle(pkg, dev):
         v, ro, vo = _reference_batch(rng, S, B, 40)
         hosts.append(({"_flat_values": torch.from_numpy(v), "_flat_row_offsets": torch.from_numpy(ro),
                        "_val_offsets": torch.from_numpy(vo)}, B))
+    # every other batch carries the order its producer made; the stager ships that one
+    for k, (h, B) in enumerate(hosts):
+        if k % 2:
+            h["_tile_order"] = pkg.make_tile_order(h["_flat_row_offsets"], B, S, torch.bfloat16, D)
     max_nnz = max(h["_flat_values"].numel() for h, _ in hosts)
     stager = pkg.InputStager(max_nnz, S, 300, dev, depth=2, order_for=(torch.bfloat16, D))
     outs = []
     for h, B in hosts:
         staged = pkg.move_model_inputs_to_device(h, dev, S, stager=stager)
         assert staged["_tile_order"].dtype == torch.int32
+        want_order = h.get("_tile_order")
+        if want_order is not None:
+            assert torch.equal(staged["_tile_order"].cpu(), want_order)
         outs.append(pkg.fused_embedding(staged, w, S).clone())
         stager.release(staged)
     torch.cuda.synchronize()
