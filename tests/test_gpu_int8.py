@@ -215,6 +215,43 @@ def test_int8_reference_layout_rounds_through_bf16(pkg, dev, odt, idx):
                           want.view(np.uint32 if odt == "f32" else np.uint16))
 
 
+def _unfused_int8_pool(values, offsets, tables, batch):
+    """Sum pooling of int8 rows with the multiply rounded before the add, acc = RN(acc + RN(q * s)),
+    in element order: the form the reference's `acc += int8_row * scale_val` (online_best/infer.py:
+    934-936) takes if its compiler does not fuse the multiply into the add."""
+    outs = []
+    for f, (q, s) in enumerate(tables):
+        acc = np.zeros((batch, q.shape[1]), np.float32)
+        for b in range(batch):
+            st, en = offsets[f * batch + b], offsets[f * batch + b + 1]
+            for i in range(st, en):
+                r = min(max(int(values[i]), 0), q.shape[0] - 1)
+                acc[b] = (acc[b] + (q[r].astype(np.float32) * s[r]).astype(np.float32)).astype(np.float32)
+        outs.append(acc)
+    return np.concatenate(outs, axis=1)
+
+
+def test_int8_within_bound_of_the_unfused_accumulation(pkg, dev):
+    """The int8 pooling equals the fused multiply-add oracle bit for bit (other tests); whether the
+    reference's Triton build fuses `acc += q * s` cannot be observed here, so the output is also
+    checked against the unfused accumulation: within the two forms' rounding difference, at most
+    one fp32 rounding of the running sum per row, L * 2^-24 * sum|q * s|, plus the output's."""
+    rng = np.random.default_rng(31)
+    F, B = 3, 40
+    tables = int8_tables(rng, F, [500], [128])
+    L, offsets = lengths_offsets(rng, F, B, 40)
+    values = ids_for(rng, L, [500])
+    out = pkg.embedding_bag_pooled(torch.from_numpy(values).to(dev), torch.from_numpy(offsets).to(dev),
+                                   dev_tables(tables, dev), pooling="sum", out_dtype=torch.float32,
+                                   long_threshold=NO_SPLIT)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    unfused = _unfused_int8_pool(values, offsets, tables, B).astype(np.float64)
+    ref64, bound = f64_int8_pool(values, offsets, tables, "sum", B)
+    assert (np.abs(got - unfused) <= 2 * bound + np.abs(ref64) * 2.0 ** -23 + 1e-30).all()
+    assert not np.array_equal(got, unfused)  # the data does tell the two forms apart
+
+
 def test_int8_matches_dequantised_float_tables_within_rounding(pkg, dev):
     """Quantise a bf16 table on the device, pool both; the int8 result tracks the bf16 one within
     the quantisation error (half a step per element, summed over the bag)."""
