@@ -1234,11 +1234,20 @@ int bags_per_tile(int variant) {
   return kRounds * r <= kWave ? kRounds * r : kWave;  // as TileShape::NB
 }
 
-constexpr int64_t kSubThreshold = 48;  // default: longer bags are split over the wavefront's subgroups
+// Default short-bag limit of the tile kernels: longer bags are split over the wavefront's lane
+// groups. Measured with host-made orders (us per launch, limit 16 / 24 / 32 / 40 / 48): bf16-2m
+// 35.2 / 34.5 / 34.8 / 35.3 / 35.7, fp32-1m 56.3 / 55.6 / 55.6 / 55.8 / 56.2; lazy-32k (no
+// order) 276.5 / 273.5 / 273.0 / 273.0 / 272.9.
+constexpr int64_t kSubThreshold = 24;
+// With length binning the limit stays 48 (capped at the block threshold): hetero-bf16 (block
+// threshold 32) ran 157.9 us at 24 against 150.6 at 32. The fused pooling + LayerNorm kernel keeps
+// 48 too: 24 measured 41.7 against 40.7 us there.
+constexpr int64_t kSubThresholdBinned = 48;
+constexpr int64_t kFusedSubThreshold = 48;
 
-int64_t default_sub_threshold(int variant) {
+int64_t default_sub_threshold(int variant, bool bins) {
   if (variant == kVarGeneric) return kNoLimit;  // the element-wise kernel never splits
-  return kSubThreshold;
+  return bins ? kSubThresholdBinned : kSubThreshold;
 }
 
 // With binning, bags longer than this go to the long kernel.
@@ -1469,10 +1478,10 @@ int run_job(const Job& j, hipStream_t stream) {
       p.idx32 = j.idx32;
       p.off32 = j.off32;
       p.round_bf16 = j.round_bf16;
-      if (v == kVarGeneric) p.sub_threshold = kNoLimit;
-      else if (j.sub_threshold == 0) p.sub_threshold = default_sub_threshold(v);
-      else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;
       const bool bins = j.use_bins && v != kVarGeneric;
+      if (v == kVarGeneric) p.sub_threshold = kNoLimit;
+      else if (j.sub_threshold == 0) p.sub_threshold = default_sub_threshold(v, bins);
+      else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;
       p.block_threshold = !bins ? kNoLimit : (j.block_threshold > 0 ? j.block_threshold : kDefaultBlockThreshold);
       p.split_threshold = !bins ? kNoLimit : (j.split_threshold > 0 ? j.split_threshold : kDefaultSplitThreshold);
       // a bag is pooled by exactly one kernel: never call a listed (long) bag short
@@ -1705,7 +1714,7 @@ extern "C" int cti_ebag_fused_all_slots_layernorm(const void* values, int32_t in
   p.batch = batch_size;
   p.pooling = pooling;
   p.num_fields = num_slots;
-  p.sub_threshold = kSubThreshold;
+  p.sub_threshold = kFusedSubThreshold;
   p.block_threshold = kNoLimit;
   p.split_threshold = kNoLimit;
   const int64_t rows = max_idx + 1;

@@ -321,6 +321,8 @@ extern "C" int cti_ebag_order_host(const void* offsets, int32_t offset_type, int
   if (nb == 0)
     return set_error(CTI_EBAG_EUNSUPPORTED, "rows of %d elements of this type take the element-wise kernel, which "
                      "follows no order", emb_dim);
+  if ((nb & (nb - 1)) != 0)  // every tiled shape holds 2 x (a power of two) bags; the walk below shifts by it
+    return set_error(CTI_EBAG_EUNSUPPORTED, "internal: %d bags per tile is not a power of two", nb);
   OrderJob oj;
   oj.offsets = offsets;
   oj.offset_type = offset_type;

@@ -7,8 +7,8 @@ which tiles start changes, so every output must equal the unordered call bit for
 stream of batches, when the batch that comes is not the one the order was made for, when the
 order was made for another tile count (not followed), and when a buffer's entries are all out of
 range. The order itself is checked on the host: its header, then each XCD range a permutation of
-itself, sorted by rows per bag in chunks of 2048 tiles. Bags of at most 48 rows are pooled by one
-lane group in element order, so batches without longer bags also match the oracle bit for bit.
+itself, sorted by rows per bag in chunks of 2048 tiles. Bags of at most SHORT rows are pooled by
+one lane group in element order, so batches without longer bags also match the oracle bit for bit.
 """
 import ctypes
 
@@ -24,6 +24,7 @@ pytestmark = pytest.mark.gpu
 
 MAGIC = 0x4F524452
 CHUNK = 2048
+SHORT = 24  # the tile kernels' default short-bag limit
 V = 3000
 
 # (table dtype, dim, fields, batch, max short-bag length, int8 tables, bags per tile)
@@ -53,7 +54,7 @@ def _batches(seed, F, B, max_len, n=4):
             L[rng.random((F, B)) < 0.7] = 0
         off = np.zeros(F * B + 1, np.int64)
         np.cumsum(L.reshape(-1), out=off[1:])
-        out.append((make_ids(rng, int(L.sum()), V), off, int(L.max(initial=0)) <= 48))
+        out.append((make_ids(rng, int(L.sum()), V), off, int(L.max(initial=0)) <= SHORT))
     return out
 
 
@@ -275,7 +276,7 @@ def _reference_batch(rng, S, B, max_len, long_every=0):
 def test_host_order_launch_equals_plain(pkg, dev, shape):
     """The drop-in launch following a host-made order equals the plain launch bit for bit, for its
     own batch, for the order of another batch of the same size, and with an order made for
-    another batch size (not followed); bags of at most 48 rows also equal the oracle."""
+    another batch size (not followed); bags of at most SHORT rows also equal the oracle."""
     tdt, D, S, B, max_len = HOST_SHAPES[shape]
     print(f"host order: {tdt} D={D} S={S} B={B}", flush=True)
     rng = np.random.default_rng(200 + shape)
@@ -303,7 +304,7 @@ def test_host_order_launch_equals_plain(pkg, dev, shape):
             pkg.fused_all_slots_embedding(dv, dvo, dro, w, got, B, D, V - 1, tile_order=order.to(dev))
             torch.cuda.synchronize()
             assert torch.equal(_bits(got), _bits(plain))
-        if int(np.diff(ro.reshape(S, B + 1), axis=1).max(initial=0)) <= 48:
+        if int(np.diff(ro.reshape(S, B + 1), axis=1).max(initial=0)) <= SHORT:
             want = orc.pool_c(v, ro, [table] * S, tdt, "sum", tdt, batch=B, val_base=vo)
             assert np.array_equal(to_np(plain, tdt), want)
 
