@@ -58,6 +58,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <type_traits>
 #include <vector>
 
 #include "ebag_device.h"
@@ -143,6 +144,8 @@ struct PoolParams {
   int32_t buffer_ok;        // every field's span_bytes is set: rows are read with buffer loads
   int32_t round_bf16;       // int8 tables: round each result to bf16 before the output type (the
                             // reference's int8 kernel stores acc.to(bfloat16), online_best/infer.py:941)
+  int32_t stream_ok;        // 256-byte rows may take streamed tiles (no binning, default short-bag
+                            // limit, walks and id offsets within 32 bits)
   FieldDesc f[kMaxFields];
 };
 
@@ -477,6 +480,226 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int fi, int local
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Streamed tile. A tile's bags are consecutive bags of one field, so with well-formed offsets
+// their rows are one contiguous run of `values`. Here the whole wavefront walks that run in
+// order, one row per load instruction (each lane holds VB bytes of every row: row_bytes = 64 *
+// VB), keeping K row loads in flight across bag boundaries: after it adds row r it issues row
+// r + K into the same registers. A bag's sum is finished (and stored) when its last row has been
+// added, so every bag is a sequential fp32 sum in element order, whatever its length. Row ids go
+// one 64-row chunk at a time through a lane vector and are broadcast with readlane; the chunk
+// after the current one is in flight meanwhile. Returns false (and does nothing) when the
+// tile's bags are not contiguous; the caller then pools the tile with pool_tile.
+// ---------------------------------------------------------------------------------------------
+template <int VB>
+__device__ __forceinline__ uint4 buffer_load_bytes(Rsrc r, unsigned int off) {
+  if constexpr (VB == 4) {
+    return make_uint4(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0), 0u, 0u, 0u);
+  } else if constexpr (VB == 8) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint4(v.x, v.y, 0u, 0u);
+  } else {
+    static_assert(VB == 16, "4, 8 or 16 bytes per lane");
+    return buffer_load16(r, off);
+  }
+}
+
+// The elements held in NW 32-bit words of one row, added in element order.
+template <typename TT, int NW>
+__device__ __forceinline__ void acc_words(float* a, const uint4& v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    if constexpr (__is_same(TT, float)) {
+      a[i] += __uint_as_float(w[i]);
+    } else if constexpr (__is_same(TT, bf16_t)) {
+      a[2 * i] += __uint_as_float(w[i] << 16);
+      a[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
+    } else {
+      a[2 * i] += f16_bits_to_f32(w[i] & 0xffffu);
+      a[2 * i + 1] += f16_bits_to_f32(w[i] >> 16);
+    }
+  }
+}
+
+// E output elements of one lane (E = 1, 2 or a multiple of 4; aligned to E * sizeof(OT) bytes, at
+// most 16).
+template <typename OT, int E>
+__device__ __forceinline__ void store_lane(OT* dst, const float* a) {
+  if constexpr (E % 4 == 0) {
+    store_out<E>(dst, a);
+  } else if constexpr (E == 1) {
+    store_one(dst, a[0]);
+  } else if constexpr (sizeof(OT) == 4) {
+    static_assert(E == 2, "two fp32 values");
+    *reinterpret_cast<uint2*>(dst) = make_uint2(__float_as_uint(a[0]), __float_as_uint(a[1]));
+  } else if constexpr (__is_same(OT, bf16_t)) {
+    static_assert(E == 2, "two 16-bit values");
+    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(a[0], a[1]);
+  } else {
+    static_assert(E == 2, "two 16-bit values");
+    *reinterpret_cast<uint32_t*>(dst) = f32_to_f16_bits(a[0]) | (f32_to_f16_bits(a[1]) << 16);
+  }
+}
+
+// Streamed tiles serve 256-byte rows of unquantised tables read with buffer loads (4 bytes per lane).
+template <typename TT, int LANES, int VPL>
+struct StreamShape {
+  static constexpr int kRowBytes = LANES * VPL * Elem<TT>::kVecBytes;
+  static constexpr bool ok = !Quantized<TT>::value && kRowBytes == 4 * kWave;
+  static constexpr int VB = ok ? kRowBytes / kWave : 4;
+  static constexpr int K = kWave / VB;  // rows in flight: 4 KiB per wavefront, 16 VGPRs of row data
+};
+
+// Raw ids of one 64-row chunk (one per lane), as loaded: converted only when the chunk is used,
+// so the load stays in flight meanwhile.
+template <typename IT>
+struct RawIds;
+template <>
+struct RawIds<int32_t> {
+  uint32_t lo;
+  __device__ __forceinline__ void load(Rsrc r, unsigned int off) { lo = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+  __device__ __forceinline__ int64_t value() const { return static_cast<int64_t>(static_cast<int32_t>(lo)); }
+};
+template <>
+struct RawIds<int64_t> {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  u32x2 w;  // one register pair, as the 8-byte load writes it
+  __device__ __forceinline__ void load(Rsrc r, unsigned int off) { w = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
+  __device__ __forceinline__ int64_t value() const { return static_cast<int64_t>(__builtin_bit_cast(uint64_t, w)); }
+};
+
+template <typename TT, typename OT, typename IT, int VB, int K, int NB>
+__device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, int local_tile) {
+  static_assert(kWave % K == 0 && K <= kWave, "K divides the 64-row id chunk");
+  static_assert(NB <= kWave, "one lane per bag");
+  constexpr int NW = VB / 4;                   // 32-bit words per lane and row
+  constexpr int E = VB / Elem<TT>::kBytes;     // elements per lane and row
+  const int gidx = p.f[fi].gidx;
+  const int64_t max_row = p.f[fi].max_row;
+  const int lane = lane_id();
+  const int64_t b0 = static_cast<int64_t>(local_tile) * NB;
+  const int nb = static_cast<int>(p.batch - b0 < NB ? p.batch - b0 : NB);
+  const bool valid = lane < nb;
+  int64_t start = 0, end = 0;
+  if (valid) bag_range(p, gidx, b0 + lane, start, end);
+  // The walk: the tile's bags' rows one after another; lane i < nb holds bag i's end in walk rows
+  // (32 bits: the host admits launches with NB * nnz < 2^31). With well-formed offsets bag i ends
+  // where bag i + 1 starts, walk row t is values[s0 + t] and bag i ends at end_i - s0; otherwise
+  // the ends are the prefix sums of the lengths.
+  const int64_t next_start = shfl_i64(start, lane + 1 < kWave ? lane + 1 : lane);
+  const bool contiguous = __ballot(valid && lane < nb - 1 && end != next_start) == 0;
+  const int64_t s0 = shfl_i64(start, 0);
+  const int len = static_cast<int>(end - start);
+  int cend = static_cast<int>(end - s0);
+  if (!contiguous) {
+    cend = len;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int t = shfl_i32(cend, lane >= d ? lane - d : lane);
+      if (lane >= d) cend += t;
+    }
+  }
+  const int T = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(cend, nb - 1));
+  const int rel_end = valid ? cend : INT32_MAX;
+  const int rel_start = cend - len;
+
+  // Row ids through a buffer over `values` (the host admits nnz * sizeof(IT) < 2^32): positions
+  // past nnz read as 0 without a memory request.
+  const uint64_t vbase = reinterpret_cast<uint64_t>(p.values);
+  const Rsrc vrsrc = make_rsrc(
+      reinterpret_cast<const char*>(
+          (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(vbase >> 32)))) << 32) |
+          static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(vbase)))),
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(p.nnz * static_cast<int64_t>(sizeof(IT))))));
+  // chunk of walk rows row0 .. row0 + 63 (row0 % 64 == 0), one per lane; lanes past the walk read
+  // whatever lies there (their ids are replaced by the pad id when the chunk is used)
+  auto load_chunk = [&](RawIds<IT>& raw, int row0) {
+    const int t = row0 + lane;
+    int64_t at;
+    if (contiguous) {
+      at = s0 + t;
+    } else {  // malformed offsets: find the bag of walk row t
+      int b = 0;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) b += t >= __builtin_amdgcn_readlane(rel_end, i) ? 1 : 0;
+      b = b < nb ? b : nb - 1;
+      at = shfl_i64(start, b) + (t - shfl_i32(rel_start, b));
+    }
+    raw.load(vrsrc, at < p.nnz ? static_cast<unsigned int>(at * static_cast<int64_t>(sizeof(IT))) : 0xffffffffu);
+  };
+
+  const Rsrc rsrc = make_rsrc(p.f[fi].table, p.f[fi].span_bytes);
+  const unsigned int shift =
+      static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(p.f[fi].row_bytes)));
+  const unsigned int r_pad = 0xffffffffu >> shift;  // offsets past the table: zeros, no request
+  const unsigned int lane_off = static_cast<unsigned int>(lane * VB);
+  OT* const out = reinterpret_cast<OT*>(p.out) + p.f[fi].out_col + lane * E;
+
+  // clamped row ids of the chunk being issued; the next chunk's raw ids are in flight meanwhile
+  RawIds<IT> raw, raw_next;
+  load_chunk(raw, 0);
+  load_chunk(raw_next, kWave);
+  unsigned int ids = lane < T ? static_cast<unsigned int>(clamp_i64(raw.value(), 0, max_row)) : r_pad;
+
+  uint4 v[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const unsigned int r = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), k));
+    v[k] = buffer_load_bytes<VB>(rsrc, (r << shift) + lane_off);
+  }
+
+  float acc[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) acc[i] = 0.f;
+  int bag = 0, prev_end = 0;
+  int next_end = __builtin_amdgcn_readlane(rel_end, 0);
+  // Store the finished bag(s) ending at walk row `row_end` (bags of zero rows included).
+  auto flush = [&](int row_end) {
+    do {
+      const int L = next_end - prev_end;
+      float r[E];
+#pragma unroll
+      for (int i = 0; i < E; ++i) r[i] = acc[i];
+      if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<E>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
+      store_lane<OT, E>(out + (b0 + bag) * p.out_row_stride, r);
+#pragma unroll
+      for (int i = 0; i < E; ++i) acc[i] = 0.f;
+      prev_end = next_end;
+      ++bag;
+      next_end = bag < nb ? __builtin_amdgcn_readlane(rel_end, bag) : INT32_MAX;
+    } while (next_end == row_end);
+  };
+  if (next_end == 0) flush(0);
+
+  for (int j = 0; j < T; j += K) {
+    const int c_issue = (j + K) & (kWave - 1);  // lane of walk row j + K in its id chunk
+    if (c_issue == 0) {
+      // rows j + K .. are in the next chunk: take it, and load the one after it
+      ids = j + K + lane < T ? static_cast<unsigned int>(clamp_i64(raw_next.value(), 0, max_row)) : r_pad;
+      load_chunk(raw_next, j + K + kWave);
+    }
+    if (j + K <= T) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        acc_words<TT, NW>(acc, v[k]);
+        if (j + k + 1 == next_end) flush(j + k + 1);
+        const unsigned int r = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k));
+        v[k] = buffer_load_bytes<VB>(rsrc, (r << shift) + lane_off);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        if (j + k < T) {
+          acc_words<TT, NW>(acc, v[k]);
+          if (j + k + 1 == next_end) flush(j + k + 1);
+        }
+      }
+    }
+  }
+}
+
 __device__ __forceinline__ void bin_handoff(const PoolParams& p) {
   if (p.bin_count && blockIdx.x == 0 && threadIdx.x == 0) {
     // hand the finished list lengths to the list kernel and zero the counters for the next call
@@ -605,7 +828,10 @@ __device__ void order_next(const PoolParams& p, int x, int chunk, OrderLds& s) {
 
 // Main kernel: one wavefront per workgroup, one tile per workgroup (after the order workgroups,
 // when the launch makes the next batch's order).
-template <typename TT, typename OT, int LANES, int VPL, bool BUF>
+// Main kernel forms: tiles pooled by pool_tile, or streamed with int32 / int64 ids.
+enum TileForm : int { kTileRanked = 0, kTileStream32 = 1, kTileStream64 = 2 };
+
+template <typename TT, typename OT, int LANES, int VPL, bool BUF, int FORM>
 __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
   __shared__ union {
     TileLdsOf<TT, LANES, VPL> tile;
@@ -622,7 +848,15 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
   }
   const int tile = ordered_tile(p, xcd_position(pos, p.num_tiles));
   const int fi = tile / p.tiles_per_field;
-  pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s.tile);
+  if constexpr (FORM != kTileRanked) {
+    using Stream = StreamShape<TT, LANES, VPL>;
+    static_assert(BUF && Stream::ok, "streamed tiles need buffer loads and 256 B - 1 KiB rows");
+    using IT = typename std::conditional<FORM == kTileStream32, int32_t, int64_t>::type;
+    pool_tile_stream<TT, OT, IT, Stream::VB, Stream::K, TileShape<TT, LANES, VPL>::NB>(p, fi,
+                                                                                       tile - fi * p.tiles_per_field);
+  } else {
+    pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s.tile);
+  }
 }
 
 // Main kernel of a mixed-width launch: the fields' rows differ in width but each is one lane
@@ -1294,10 +1528,16 @@ void launch_shape(const PoolParams& p, const LongList* l, hipStream_t s) {
   if (l) launch_bins(p, *l, s);
   const dim3 grid(static_cast<unsigned>(p.num_tiles) + (p.next_order ? static_cast<unsigned>(p.order_blocks) : 0u)),
       block(kMainThreads);
-  if (p.buffer_ok)
-    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true>), grid, block, 0, s, p);
+  constexpr bool kStream = StreamShape<TT, LANES, VPL>::ok;
+  const bool stream = kStream && p.stream_ok && p.buffer_ok;
+  if (stream && p.idx32)
+    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true, kStream ? kTileStream32 : kTileRanked>), grid, block, 0, s, p);
+  else if (stream)
+    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true, kStream ? kTileStream64 : kTileRanked>), grid, block, 0, s, p);
+  else if (p.buffer_ok)
+    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true, kTileRanked>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, false>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, false, kTileRanked>), grid, block, 0, s, p);
   if (l) {
     constexpr int LW = VPL >= 4 ? 4 : 8;  // keeps the LDS partials at <= 32 KB
     hipLaunchKernelGGL((pool_long_kernel<TT, OT, LW, FixedRows<TT, OT, LANES, VPL, LW>>), dim3(list_blocks(p)),
@@ -1405,6 +1645,23 @@ int validate_tables(const Job& j) {
 
 int64_t workspace_bytes(int64_t batch, int32_t num_fields);
 
+// The variant whose rows are 256 bytes (16 lanes of one 16-byte vector): the streamed tiles' shape
+// for fp32 / bf16 / fp16 tables.
+constexpr int kVarStream = 4;
+static_assert(StreamShape<float, 1 << kVarStream, 1>::ok && StreamShape<bf16_t, 1 << kVarStream, 1>::ok &&
+                  StreamShape<f16_t, 1 << kVarStream, 1>::ok && !StreamShape<i8_t, 1 << kVarStream, 1>::ok &&
+                  TileShape<bf16_t, 1 << kVarStream, 1>::NB == kRounds * (kWave / 16),
+              "the streamed shape is variant kVarStream");
+
+// Whether a job's 256-byte-row fields may take streamed tiles (launch_shape also needs buffer
+// loads over every table of their launch): no binning, the default short-bag limit, unquantised
+// tables, and walks / id offsets that fit 32 bits.
+bool stream_variant_allowed(const Job& j) {
+  const int64_t nb = kRounds * (kWave / 16);  // bags per tile of the 256-byte shape
+  return !j.use_bins && j.sub_threshold == 0 && j.tdt != CTI_EBAG_I8 && j.nnz < INT32_MAX / nb &&
+         j.nnz * (j.idx32 ? 4 : 8) < (int64_t{1} << 32);
+}
+
 int run_job(const Job& j, hipStream_t stream) {
   if (j.batch == 0 || j.num_fields == 0) return CTI_EBAG_OK;
   const int tb = dtype_bytes(j.tdt), ob = dtype_bytes(j.odt);
@@ -1425,8 +1682,12 @@ int run_job(const Job& j, hipStream_t stream) {
   // whose rows are one lane vector per lane but of different widths form one mixed group.
   std::vector<int> var(j.num_fields);
   for (int f = 0; f < j.num_fields; ++f) var[f] = pick_variant(j.tables[f], tb, ob, j.out, j.out_row_stride);
+  // Fields of 256-byte rows that may take streamed tiles keep a launch of their own, so a field is
+  // pooled the same way whatever other fields share the call.
+  const bool stream_apart = stream_variant_allowed(j);
   int one_vec_shapes = 0;
   for (int v = kMixedLo; v <= kMixedHi; ++v) {
+    if (stream_apart && v == kVarStream) continue;
     for (int f = 0; f < j.num_fields; ++f) {
       if (var[f] == v) {
         ++one_vec_shapes;
@@ -1457,10 +1718,12 @@ int run_job(const Job& j, hipStream_t stream) {
     if (v == kVarMixed) {
       if (!mixed) continue;
       // widest rows first (fewest bags per tile), so those tiles start first
-      for (int w = kMixedHi; w >= kMixedLo; --w)
+      for (int w = kMixedHi; w >= kMixedLo; --w) {
+        if (stream_apart && w == kVarStream) continue;
         for (int f = 0; f < j.num_fields; ++f) if (var[f] == w) fields.push_back(f);
+      }
     } else {
-      if (mixed && v >= kMixedLo && v <= kMixedHi) continue;
+      if (mixed && v >= kMixedLo && v <= kMixedHi && !(stream_apart && v == kVarStream)) continue;
       for (int f = 0; f < j.num_fields; ++f) if (var[f] == v) fields.push_back(f);
     }
     for (size_t c0 = 0; c0 < fields.size(); c0 += kMaxFields) {
@@ -1479,6 +1742,7 @@ int run_job(const Job& j, hipStream_t stream) {
       p.off32 = j.off32;
       p.round_bf16 = j.round_bf16;
       const bool bins = j.use_bins && v != kVarGeneric;
+      p.stream_ok = stream_variant_allowed(j) ? 1 : 0;
       if (v == kVarGeneric) p.sub_threshold = kNoLimit;
       else if (j.sub_threshold == 0) p.sub_threshold = default_sub_threshold(v, bins);
       else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;

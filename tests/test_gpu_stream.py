@@ -1,0 +1,132 @@
+"""Streamed tiles on the GPU: 256-byte rows (bf16 / fp16 D = 128, fp32 D = 64) without binning and
+with the default short-bag limit, where a wavefront walks a tile's rows in order across bag
+boundaries.
+
+Bar: every bag, whatever its length, equals the oracle's sequential fp32 sum bit for bit (sum and
+mean, every output type, int32 and int64 ids, with and without a dispatch order); malformed
+offsets (decreasing, negative, past nnz), whose bags are not one contiguous run, pool exactly as
+the oracle clamps them, in the global and the reference layout; an explicit short-bag limit
+takes the length-ranked tiles instead.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _cases import make_ids, make_table, random_case
+from oracle import ebag_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TORCH_DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+SHAPES = [("bf16", 128), ("f16", 128), ("f32", 64)]
+
+
+def to_dev(arr, tdt, dev):
+    t = torch.from_numpy(np.ascontiguousarray(arr))
+    if tdt != "f32":
+        t = t.view(torch.int16).view(TORCH_DT[tdt])
+    return t.to(dev)
+
+
+def to_np(t, odt):
+    t = t.cpu()
+    return t.numpy() if odt == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+
+
+def pooled(pkg, dev, values, offsets, tables, tdt, pooling, odt, idx=torch.int64, **kw):
+    v = torch.from_numpy(np.ascontiguousarray(values)).to(dev, idx)
+    o = torch.from_numpy(np.ascontiguousarray(offsets)).to(dev)
+    out = pkg.embedding_bag_pooled(v, o, [to_dev(t, tdt, dev) for t in tables], pooling=pooling,
+                                   out_dtype=TORCH_DT[odt], **kw)
+    torch.cuda.synchronize()
+    return to_np(out, odt)
+
+
+@pytest.mark.parametrize("tdt,D", SHAPES)
+@pytest.mark.parametrize("odt", ["same", "f32"])
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+@pytest.mark.parametrize("idx", [torch.int64, torch.int32])
+def test_every_length_bitwise(pkg, dev, tdt, D, odt, pooling, idx):
+    odt = tdt if odt == "same" else odt
+    print(f"stream {tdt} D={D} out={odt} {pooling} {idx}", flush=True)
+    # lengths 0..60 with every fifth bag 300 rows: walks of many 64-row id chunks, bags ending
+    # anywhere inside a 16-row step, runs of empty bags, and a short last tile (B = 37)
+    case = random_case(D + len(tdt) + len(pooling), F=5, B=37, dims=(D,), V=(900,), max_len=60, tdt=tdt,
+                       long_every=5, long_len=300)
+    values = case.values if idx == torch.int64 else np.clip(case.values, -2 ** 31, 2 ** 31 - 1).astype(np.int32)
+    want = orc.pool_c(values, case.offsets, case.tables, tdt, pooling, odt)
+    got = pooled(pkg, dev, values, case.offsets, case.tables, tdt, pooling, odt, idx=idx)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("tdt,D", SHAPES)
+def test_long_runs_and_empty_tiles(pkg, dev, tdt, D):
+    """One bag of 5,000 rows among empty ones, tiles with no rows at all, and a single sample."""
+    rng = np.random.default_rng(7)
+    F, B, V = 3, 19, 4000
+    L = np.zeros((F, B), np.int64)
+    L[0, 9] = 5000
+    L[1, :] = rng.integers(0, 3, B)
+    L[2, 17:] = [64, 65]
+    ids = make_ids(rng, int(L.sum()), V)
+    offsets = np.concatenate([[0], np.cumsum(L.reshape(-1))]).astype(np.int64)
+    tables = [make_table(rng, V, D, tdt) for _ in range(F)]
+    for pooling in ("sum", "mean"):
+        want = orc.pool_c(ids, offsets, tables, tdt, pooling, tdt)
+        assert np.array_equal(pooled(pkg, dev, ids, offsets, tables, tdt, pooling, tdt), want), pooling
+    one = np.array([0, 70], np.int64)
+    want = orc.pool_c(ids[:70], one, tables[:1], tdt, "sum", tdt)
+    assert np.array_equal(pooled(pkg, dev, ids[:70], one, tables[:1], tdt, "sum", tdt), want)
+
+
+def _malformed(offsets, nnz, rng):
+    """Offsets that step back, go negative and run past nnz in places (each bag is then what the
+    clamps make of it: start in [0, nnz], end in [start, nnz])."""
+    o = offsets.copy()
+    n = o.size
+    for k in rng.choice(np.arange(1, n - 1), size=max(1, n // 6), replace=False):
+        o[k] = o[k] - int(rng.integers(1, 40))  # a decrease (possibly below zero)
+    o[rng.integers(1, n - 1)] = -5
+    o[rng.integers(1, n - 1)] = nnz + 9
+    return o
+
+
+@pytest.mark.parametrize("tdt,D,kind", [("bf16", 128, "normal"), ("f32", 64, "normal"), ("bf16", 256, "int")])
+def test_malformed_global_offsets_match_oracle(pkg, dev, tdt, D, kind):
+    # 256-wide bf16 rows take the ranked tiles, which split the long bags the bad offsets make:
+    # integer rows keep those sums exact
+    print(f"malformed global {tdt} D={D}", flush=True)
+    rng = np.random.default_rng(D + 1)
+    case = random_case(D + 2, F=4, B=45, dims=(D,), V=(700,), max_len=20, tdt=tdt, kind=kind)
+    bad = _malformed(case.offsets, case.values.size, rng)
+    for pooling in ("sum", "mean"):
+        want = orc.pool_c(case.values, bad, case.tables, tdt, pooling, tdt)
+        got = pooled(pkg, dev, case.values, bad, case.tables, tdt, pooling, tdt)
+        assert np.array_equal(got, want), pooling
+
+
+def test_malformed_reference_layout_matches_oracle(pkg, dev):
+    rng = np.random.default_rng(3)
+    S, B, V, D = 6, 30, 800, 128
+    case = random_case(11, F=S, B=B, dims=(D,), V=(V,), max_len=20, tdt="bf16")
+    ro, vo = case.reference_layout()
+    ro = _malformed(ro, case.values.size, rng)
+    w = torch.from_numpy(case.tables[0].view(np.int16)).view(torch.bfloat16).to(dev)
+    out = torch.empty((B, S * D), dtype=torch.bfloat16, device=dev)
+    pkg.fused_all_slots_embedding(torch.from_numpy(case.values).to(dev), torch.from_numpy(vo).to(dev),
+                                  torch.from_numpy(ro).to(dev), w, out, B, D, V - 1)
+    torch.cuda.synchronize()
+    want = orc.pool_c(case.values, ro, [case.tables[0]] * S, "bf16", "sum", "bf16", batch=B, val_base=vo)
+    assert np.array_equal(to_np(out, "bf16"), want)
+
+
+def test_explicit_short_bag_limit_takes_the_ranked_tiles(pkg, dev):
+    """With a short-bag limit of the caller's, bags above it are split over the wavefront's lane
+    groups (sums within the reassociation bound, not the sequential sum); the default streams."""
+    case = random_case(5, F=3, B=40, dims=(128,), V=(600,), max_len=10, tdt="bf16", long_every=4, long_len=200)
+    args = (case.values, case.offsets, case.tables, "bf16", "sum", "f32")
+    want = orc.pool_c(*args)
+    assert np.array_equal(pooled(pkg, dev, *args), want)
+    split = pooled(pkg, dev, *args, long_threshold=-1)
+    assert not np.array_equal(split, want)  # the split sums round differently somewhere
+    np.testing.assert_allclose(split, want, rtol=1e-4, atol=1e-3)
