@@ -28,6 +28,14 @@
 //     completes under the current chunk's row loads. Tables under 4 GiB with power-of-two row sizes are read with buffer
 //     loads: a row's offset is one shift-add, and rows past a bag's end use an out-of-range offset
 //     that returns zeros without a memory request (no per-row branch).
+//   * Streamed tiles (256-byte rows of fp32 / bf16 / fp16 tables, without binning and with the
+//     default short-bag limit): the same tiles, but the wavefront walks the tile's rows in order
+//     across bag boundaries (with well-formed offsets they are one contiguous run of `values`),
+//     each lane holding 4 bytes of every row, one row per load instruction, 16 rows in flight;
+//     a bag is stored when its last row has been added, so every bag, whatever its length, is a
+//     sequential fp32 sum in element order. Row ids come one 64-row chunk at a time through
+//     buffer loads over `values` (the next chunk in flight) and are broadcast with readlane.
+//     No lane group waits for another's longer bag and no bag is split.
 //   * Dispatch order (optional): a launch can follow a tile order made one batch ahead, in which
 //     each XCD starts its tiles with the most rows per bag, and make the next batch's order in a
 //     few extra workgroups at its first dispatch positions. It shortens the launch's drain; the
@@ -613,8 +621,8 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
           (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(vbase >> 32)))) << 32) |
           static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(vbase)))),
       static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(p.nnz * static_cast<int64_t>(sizeof(IT))))));
-  // chunk of walk rows row0 .. row0 + 63 (row0 % 64 == 0), one per lane; lanes past the walk read
-  // whatever lies there (their ids are replaced by the pad id when the chunk is used)
+  // chunk of walk rows row0 .. row0 + 63 (row0 % 64 == 0), one per lane; lanes past the walk
+  // request nothing (their ids are replaced by the pad id when the chunk is used)
   auto load_chunk = [&](RawIds<IT>& raw, int row0) {
     const int t = row0 + lane;
     int64_t at;
@@ -627,7 +635,7 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
       b = b < nb ? b : nb - 1;
       at = shfl_i64(start, b) + (t - shfl_i32(rel_start, b));
     }
-    raw.load(vrsrc, at < p.nnz ? static_cast<unsigned int>(at * static_cast<int64_t>(sizeof(IT))) : 0xffffffffu);
+    raw.load(vrsrc, t < T && at < p.nnz ? static_cast<unsigned int>(at * static_cast<int64_t>(sizeof(IT))) : 0xffffffffu);
   };
 
   const Rsrc rsrc = make_rsrc(p.f[fi].table, p.f[fi].span_bytes);
