@@ -551,13 +551,14 @@ __device__ __forceinline__ void store_lane(OT* dst, const float* a) {
   }
 }
 
-// Streamed tiles serve 256-byte rows of unquantised tables read with buffer loads (4 bytes per lane).
+// Streamed tiles serve 256-byte rows of fp32 / bf16 / fp16 tables read with buffer loads (4 bytes
+// per lane).
 template <typename TT, int LANES, int VPL>
 struct StreamShape {
   static constexpr int kRowBytes = LANES * VPL * Elem<TT>::kVecBytes;
-  static constexpr bool ok = !Quantized<TT>::value && kRowBytes == 4 * kWave;
+  static constexpr bool ok = !Quantized<TT>::value && LANES == 16 && VPL == 1;  // 256-byte rows
   static constexpr int VB = ok ? kRowBytes / kWave : 4;
-  static constexpr int K = kWave / VB;  // rows in flight: 4 KiB per wavefront, 16 VGPRs of row data
+  static constexpr int K = 16;  // rows in flight: 16 VGPRs of row data
 };
 
 // Raw ids of one 64-row chunk (one per lane), as loaded: converted only when the chunk is used,
@@ -578,28 +579,30 @@ struct RawIds<int64_t> {
   __device__ __forceinline__ int64_t value() const { return static_cast<int64_t>(__builtin_bit_cast(uint64_t, w)); }
 };
 
-template <typename TT, typename OT, typename IT, int VB, int K, int NB>
-__device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, int local_tile) {
+// Walks the rows of nb <= NB bags in order, bag after bag: lane i < nb describes bag i, the rows
+// values[start, end). Each lane holds VB bytes of every row (row_bytes = 64 * VB, read through
+// `rsrc`, `shift` = log2(row_bytes)); K row loads stay in flight across bag boundaries. When the
+// last row of bag i has been added (at once for an empty bag) it calls store(i, r) with the bag's
+// E = VB / sizeof(TT) results of this lane (divided by the length for mean pooling), i rising.
+// Walk rows are counted in 32 bits: the bags hold fewer than 2^31 rows in all (host).
+template <typename TT, typename IT, int VB, int K, int NB, typename Store>
+__device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsigned int shift, int64_t max_row, int nb,
+                                            int64_t start, int64_t end, Store&& store) {
   static_assert(kWave % K == 0 && K <= kWave, "K divides the 64-row id chunk");
   static_assert(NB <= kWave, "one lane per bag");
+  static_assert(!Quantized<TT>::value, "unquantised rows");
   constexpr int NW = VB / 4;                   // 32-bit words per lane and row
   constexpr int E = VB / Elem<TT>::kBytes;     // elements per lane and row
-  const int gidx = p.f[fi].gidx;
-  const int64_t max_row = p.f[fi].max_row;
   const int lane = lane_id();
-  const int64_t b0 = static_cast<int64_t>(local_tile) * NB;
-  const int nb = static_cast<int>(p.batch - b0 < NB ? p.batch - b0 : NB);
   const bool valid = lane < nb;
-  int64_t start = 0, end = 0;
-  if (valid) bag_range(p, gidx, b0 + lane, start, end);
-  // The walk: the tile's bags' rows one after another; lane i < nb holds bag i's end in walk rows
-  // (32 bits: the host admits launches with NB * nnz < 2^31). With well-formed offsets bag i ends
-  // where bag i + 1 starts, walk row t is values[s0 + t] and bag i ends at end_i - s0; otherwise
-  // the ends are the prefix sums of the lengths.
+  if (nb <= 0) return;
+  // Lane i < nb holds bag i's end in walk rows. With well-formed offsets (consecutive bags of one
+  // field) bag i ends where bag i + 1 starts, walk row t is values[s0 + t] and bag i ends at
+  // end_i - s0; otherwise the ends are the prefix sums of the lengths.
   const int64_t next_start = shfl_i64(start, lane + 1 < kWave ? lane + 1 : lane);
   const bool contiguous = __ballot(valid && lane < nb - 1 && end != next_start) == 0;
   const int64_t s0 = shfl_i64(start, 0);
-  const int len = static_cast<int>(end - start);
+  const int len = valid ? static_cast<int>(end - start) : 0;
   int cend = static_cast<int>(end - s0);
   if (!contiguous) {
     cend = len;
@@ -628,7 +631,7 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
     int64_t at;
     if (contiguous) {
       at = s0 + t;
-    } else {  // malformed offsets: find the bag of walk row t
+    } else {  // find the bag of walk row t
       int b = 0;
 #pragma unroll
       for (int i = 0; i < NB; ++i) b += t >= __builtin_amdgcn_readlane(rel_end, i) ? 1 : 0;
@@ -638,12 +641,8 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
     raw.load(vrsrc, t < T && at < p.nnz ? static_cast<unsigned int>(at * static_cast<int64_t>(sizeof(IT))) : 0xffffffffu);
   };
 
-  const Rsrc rsrc = make_rsrc(p.f[fi].table, p.f[fi].span_bytes);
-  const unsigned int shift =
-      static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(p.f[fi].row_bytes)));
   const unsigned int r_pad = 0xffffffffu >> shift;  // offsets past the table: zeros, no request
   const unsigned int lane_off = static_cast<unsigned int>(lane * VB);
-  OT* const out = reinterpret_cast<OT*>(p.out) + p.f[fi].out_col + lane * E;
 
   // clamped row ids of the chunk being issued; the next chunk's raw ids are in flight meanwhile
   RawIds<IT> raw, raw_next;
@@ -663,7 +662,7 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
   for (int i = 0; i < E; ++i) acc[i] = 0.f;
   int bag = 0, prev_end = 0;
   int next_end = __builtin_amdgcn_readlane(rel_end, 0);
-  // Store the finished bag(s) ending at walk row `row_end` (bags of zero rows included).
+  // Finish the bag(s) ending at walk row `row_end` (bags of zero rows included).
   auto flush = [&](int row_end) {
     do {
       const int L = next_end - prev_end;
@@ -671,7 +670,7 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
 #pragma unroll
       for (int i = 0; i < E; ++i) r[i] = acc[i];
       if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<E>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
-      store_lane<OT, E>(out + (b0 + bag) * p.out_row_stride, r);
+      store(bag, r);
 #pragma unroll
       for (int i = 0; i < E; ++i) acc[i] = 0.f;
       prev_end = next_end;
@@ -706,6 +705,24 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
       }
     }
   }
+}
+
+// A tile of NB consecutive bags of one field, streamed (see stream_walk).
+template <typename TT, typename OT, typename IT, int VB, int K, int NB>
+__device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, int local_tile) {
+  constexpr int E = VB / Elem<TT>::kBytes;
+  const int lane = lane_id();
+  const int64_t b0 = static_cast<int64_t>(local_tile) * NB;
+  const int nb = static_cast<int>(p.batch - b0 < NB ? p.batch - b0 : NB);
+  int64_t start = 0, end = 0;
+  if (lane < nb) bag_range(p, p.f[fi].gidx, b0 + lane, start, end);
+  const Rsrc rsrc = make_rsrc(p.f[fi].table, p.f[fi].span_bytes);
+  const unsigned int shift =
+      static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(p.f[fi].row_bytes)));
+  OT* const out = reinterpret_cast<OT*>(p.out) + p.f[fi].out_col + lane * E;
+  stream_walk<TT, IT, VB, K, NB>(p, rsrc, shift, p.f[fi].max_row, nb, start, end, [&](int bag, const float* r) {
+    store_lane<OT, E>(out + (b0 + bag) * p.out_row_stride, r);
+  });
 }
 
 __device__ __forceinline__ void bin_handoff(const PoolParams& p) {
@@ -1661,11 +1678,11 @@ static_assert(StreamShape<float, 1 << kVarStream, 1>::ok && StreamShape<bf16_t, 
                   TileShape<bf16_t, 1 << kVarStream, 1>::NB == kRounds * (kWave / 16),
               "the streamed shape is variant kVarStream");
 
-// Whether a job's 256-byte-row fields may take streamed tiles (launch_shape also needs buffer
-// loads over every table of their launch): no binning, the default short-bag limit, unquantised
-// tables, and walks / id offsets that fit 32 bits.
+// Whether a job's fields of the streamed shape may take streamed tiles (launch_shape also needs
+// buffer loads over every table of their launch): no binning, the default short-bag limit,
+// unquantised tables, and walks / id offsets that fit 32 bits.
 bool stream_variant_allowed(const Job& j) {
-  const int64_t nb = kRounds * (kWave / 16);  // bags per tile of the 256-byte shape
+  const int64_t nb = kRounds * (kWave / 16);  // bags per tile of the streamed shape
   return !j.use_bins && j.sub_threshold == 0 && j.tdt != CTI_EBAG_I8 && j.nnz < INT32_MAX / nb &&
          j.nnz * (j.idx32 ? 4 : 8) < (int64_t{1} << 32);
 }
