@@ -30,6 +30,26 @@ __device__ __forceinline__ int64_t wrap32(int64_t x, bool wrap) {
   return wrap ? static_cast<int64_t>(static_cast<int32_t>(static_cast<uint32_t>(static_cast<uint64_t>(x)))) : x;
 }
 
+// Elements e and e + 1 of src[0, n) (e < n; the second is 0 past the end), and their store as
+// dst[i] = post + wrap32(src[i] + add).
+__device__ __forceinline__ I64Pair load_pair(const int64_t* __restrict__ src, int64_t e, int64_t n) {
+  I64Pair v;
+  if (e + 1 < n) {
+    __builtin_memcpy(&v, src + e, sizeof(v));
+  } else {
+    v.a = src[e];
+    v.b = 0;
+  }
+  return v;
+}
+__device__ __forceinline__ void store_pair(int64_t* __restrict__ dst, int64_t e, int64_t n, I64Pair v, int64_t add,
+                                           bool wrap, int64_t post) {
+  v.a = post + wrap32(v.a + add, wrap);
+  v.b = post + wrap32(v.b + add, wrap);
+  if (e + 1 < n) __builtin_memcpy(dst + e, &v, sizeof(v));
+  else dst[e] = v.a;
+}
+
 // dst[i] = post + wrap32(src[i] + add) for i < n; grid-stride item j covers elements 2j and 2j+1.
 __device__ __forceinline__ void copy_add_i64(const int64_t* __restrict__ src, int64_t* __restrict__ dst, int64_t n,
                                              int64_t add, int64_t j0, int64_t stride, bool wrap = false,
@@ -127,6 +147,19 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const MergeParams p) {
   const int64_t work = n_here > p.bsub[k] ? n_here : p.bsub[k];
   if (blockIdx.x > 0 && static_cast<int64_t>(blockIdx.x) * kThreads * 2 >= work) return;
 
+  // This thread's first pair of values and of row offsets is read before the slot's destination
+  // (which needs the sizes of all earlier slots) is summed, so the two latencies overlap.
+  const int64_t Bk = p.bsub[k];
+  const int64_t n = n_here;
+  const int64_t src0 = slot_start(p, s, k);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kThreads + t;
+  const int64_t e0 = 2 * i0;
+  const int64_t* __restrict__ so = p.ro[k] + static_cast<int64_t>(s) * (Bk + 1);
+  I64Pair v0 = {0, 0}, o0 = {0, 0};
+  if (e0 < n) v0 = load_pair(p.vals[k] + src0, e0, n);
+  if (e0 < Bk) o0 = load_pair(so, e0, Bk);
+
   // before: values of slots < s (all sub-batches); vb: slot s of sub-batches < k; tot: slot s.
   int64_t before = 0, vb = 0, tot = 0;
   const int pairs = (s + 1) * K;
@@ -163,20 +196,20 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const MergeParams p) {
   }
 
   const int64_t B = p.batch;
-  const int64_t Bk = p.bsub[k];
-  const int64_t n = n_here;
-  const int64_t src0 = slot_start(p, s, k);
   const int64_t dst0 = before + vb;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kThreads + t;
-  const int64_t* __restrict__ so = p.ro[k] + static_cast<int64_t>(s) * (Bk + 1);
   const bool w = p.wrap32 != 0;
-  copy_add_i64(p.vals[k] + src0, p.flat_values + dst0, n, 0, i0, stride, w);
-  copy_add_i64(so, p.flat_row_offsets + static_cast<int64_t>(s) * (B + 1) + p.bbase[k], Bk, vb, i0, stride, w);
+  int64_t* const dst_ro = p.flat_row_offsets + static_cast<int64_t>(s) * (B + 1) + p.bbase[k];
   // global form: slot base + the (possibly wrapped) slot-local offset, as a reader of the merged
   // flat layout would add them
-  if (p.global_offsets)
-    copy_add_i64(so, p.global_offsets + static_cast<int64_t>(s) * B + p.bbase[k], Bk, vb, i0, stride, w, before);
+  int64_t* const dst_go = p.global_offsets ? p.global_offsets + static_cast<int64_t>(s) * B + p.bbase[k] : nullptr;
+  if (e0 < n) store_pair(p.flat_values + dst0, e0, n, v0, 0, w, 0);
+  if (e0 < Bk) {
+    store_pair(dst_ro, e0, Bk, o0, vb, w, 0);
+    if (dst_go) store_pair(dst_go, e0, Bk, o0, vb, w, before);
+  }
+  copy_add_i64(p.vals[k] + src0, p.flat_values + dst0, n, 0, i0 + stride, stride, w);
+  copy_add_i64(so, dst_ro, Bk, vb, i0 + stride, stride, w);
+  if (dst_go) copy_add_i64(so, dst_go, Bk, vb, i0 + stride, stride, w, before);
   if (i0 == 0) {
     if (k == K - 1) p.flat_row_offsets[static_cast<int64_t>(s) * (B + 1) + B] = wrap32(tot, w);
     if (k == 0) p.val_offsets[s] = before;
