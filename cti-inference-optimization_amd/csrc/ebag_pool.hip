@@ -499,45 +499,25 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int fi, int local
 // after the current one is in flight meanwhile. Returns false (and does nothing) when the
 // tile's bags are not contiguous; the caller then pools the tile with pool_tile.
 // ---------------------------------------------------------------------------------------------
-template <int VB>
-__device__ __forceinline__ uint4 buffer_load_bytes(Rsrc r, unsigned int off) {
-  if constexpr (VB == 4) {
-    return make_uint4(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0), 0u, 0u, 0u);
-  } else if constexpr (VB == 8) {
-    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-    return make_uint4(v.x, v.y, 0u, 0u);
+// The elements of a row that one 32-bit word holds (one fp32, or two bf16 / fp16), added in
+// element order.
+template <typename TT>
+__device__ __forceinline__ void acc_word(float* a, uint32_t w) {
+  if constexpr (__is_same(TT, float)) {
+    a[0] += __uint_as_float(w);
+  } else if constexpr (__is_same(TT, bf16_t)) {
+    a[0] += __uint_as_float(w << 16);
+    a[1] += __uint_as_float(w & 0xffff0000u);
   } else {
-    static_assert(VB == 16, "4, 8 or 16 bytes per lane");
-    return buffer_load16(r, off);
+    a[0] += f16_bits_to_f32(w & 0xffffu);
+    a[1] += f16_bits_to_f32(w >> 16);
   }
 }
 
-// The elements held in NW 32-bit words of one row, added in element order.
-template <typename TT, int NW>
-__device__ __forceinline__ void acc_words(float* a, const uint4& v) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    if constexpr (__is_same(TT, float)) {
-      a[i] += __uint_as_float(w[i]);
-    } else if constexpr (__is_same(TT, bf16_t)) {
-      a[2 * i] += __uint_as_float(w[i] << 16);
-      a[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
-    } else {
-      a[2 * i] += f16_bits_to_f32(w[i] & 0xffffu);
-      a[2 * i + 1] += f16_bits_to_f32(w[i] >> 16);
-    }
-  }
-}
-
-// E output elements of one lane (E = 1, 2 or a multiple of 4; aligned to E * sizeof(OT) bytes, at
-// most 16).
+// E = 1 or 2 output elements of one lane (aligned to E * sizeof(OT) bytes).
 template <typename OT, int E>
 __device__ __forceinline__ void store_lane(OT* dst, const float* a) {
-  if constexpr (E % 4 == 0) {
-    store_out<E>(dst, a);
-  } else if constexpr (E == 1) {
+  if constexpr (E == 1) {
     store_one(dst, a[0]);
   } else if constexpr (sizeof(OT) == 4) {
     static_assert(E == 2, "two fp32 values");
@@ -551,13 +531,11 @@ __device__ __forceinline__ void store_lane(OT* dst, const float* a) {
   }
 }
 
-// Streamed tiles serve 256-byte rows of fp32 / bf16 / fp16 tables read with buffer loads (4 bytes
-// per lane).
+// Streamed tiles serve 256-byte rows of fp32 / bf16 / fp16 tables read with buffer loads: a row is
+// one 4-byte word per lane.
 template <typename TT, int LANES, int VPL>
 struct StreamShape {
-  static constexpr int kRowBytes = LANES * VPL * Elem<TT>::kVecBytes;
   static constexpr bool ok = !Quantized<TT>::value && LANES == 16 && VPL == 1;  // 256-byte rows
-  static constexpr int VB = ok ? kRowBytes / kWave : 4;
   static constexpr int K = 16;  // rows in flight: 16 VGPRs of row data
 };
 
@@ -580,19 +558,18 @@ struct RawIds<int64_t> {
 };
 
 // Walks the rows of nb <= NB bags in order, bag after bag: lane i < nb describes bag i, the rows
-// values[start, end). Each lane holds VB bytes of every row (row_bytes = 64 * VB, read through
-// `rsrc`, `shift` = log2(row_bytes)); K row loads stay in flight across bag boundaries. When the
-// last row of bag i has been added (at once for an empty bag) it calls store(i, r) with the bag's
-// E = VB / sizeof(TT) results of this lane (divided by the length for mean pooling), i rising.
+// values[start, end). Each lane holds 4 bytes of every 256-byte row (read through `rsrc`, `shift`
+// = log2 of the row stride); K row loads stay in flight across bag boundaries. When the last row
+// of bag i has been added (at once for an empty bag) it calls store(i, r) with the bag's
+// E = 4 / sizeof(TT) results of this lane (divided by the length for mean pooling), i rising.
 // Walk rows are counted in 32 bits: the bags hold fewer than 2^31 rows in all (host).
-template <typename TT, typename IT, int VB, int K, int NB, typename Store>
+template <typename TT, typename IT, int K, int NB, typename Store>
 __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsigned int shift, int64_t max_row, int nb,
                                             int64_t start, int64_t end, Store&& store) {
   static_assert(kWave % K == 0 && K <= kWave, "K divides the 64-row id chunk");
   static_assert(NB <= kWave, "one lane per bag");
   static_assert(!Quantized<TT>::value, "unquantised rows");
-  constexpr int NW = VB / 4;                   // 32-bit words per lane and row
-  constexpr int E = VB / Elem<TT>::kBytes;     // elements per lane and row
+  constexpr int E = 4 / Elem<TT>::kBytes;  // elements per lane and row
   const int lane = lane_id();
   const bool valid = lane < nb;
   if (nb <= 0) return;
@@ -642,7 +619,7 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
   };
 
   const unsigned int r_pad = 0xffffffffu >> shift;  // offsets past the table: zeros, no request
-  const unsigned int lane_off = static_cast<unsigned int>(lane * VB);
+  const unsigned int lane_off = static_cast<unsigned int>(lane * 4);
 
   // clamped row ids of the chunk being issued; the next chunk's raw ids are in flight meanwhile
   RawIds<IT> raw, raw_next;
@@ -650,11 +627,11 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
   load_chunk(raw_next, kWave);
   unsigned int ids = lane < T ? static_cast<unsigned int>(clamp_i64(raw.value(), 0, max_row)) : r_pad;
 
-  uint4 v[K];
+  uint32_t v[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const unsigned int r = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), k));
-    v[k] = buffer_load_bytes<VB>(rsrc, (r << shift) + lane_off);
+    v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, (r << shift) + lane_off, 0, 0);
   }
 
   float acc[E];
@@ -690,16 +667,16 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
     if (j + K <= T) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        acc_words<TT, NW>(acc, v[k]);
+        acc_word<TT>(acc, v[k]);
         if (j + k + 1 == next_end) flush(j + k + 1);
         const unsigned int r = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k));
-        v[k] = buffer_load_bytes<VB>(rsrc, (r << shift) + lane_off);
+        v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, (r << shift) + lane_off, 0, 0);
       }
     } else {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         if (j + k < T) {
-          acc_words<TT, NW>(acc, v[k]);
+          acc_word<TT>(acc, v[k]);
           if (j + k + 1 == next_end) flush(j + k + 1);
         }
       }
@@ -708,9 +685,9 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
 }
 
 // A tile of NB consecutive bags of one field, streamed (see stream_walk).
-template <typename TT, typename OT, typename IT, int VB, int K, int NB>
+template <typename TT, typename OT, typename IT, int K, int NB>
 __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, int local_tile) {
-  constexpr int E = VB / Elem<TT>::kBytes;
+  constexpr int E = 4 / Elem<TT>::kBytes;
   const int lane = lane_id();
   const int64_t b0 = static_cast<int64_t>(local_tile) * NB;
   const int nb = static_cast<int>(p.batch - b0 < NB ? p.batch - b0 : NB);
@@ -720,7 +697,7 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
   const unsigned int shift =
       static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(p.f[fi].row_bytes)));
   OT* const out = reinterpret_cast<OT*>(p.out) + p.f[fi].out_col + lane * E;
-  stream_walk<TT, IT, VB, K, NB>(p, rsrc, shift, p.f[fi].max_row, nb, start, end, [&](int bag, const float* r) {
+  stream_walk<TT, IT, K, NB>(p, rsrc, shift, p.f[fi].max_row, nb, start, end, [&](int bag, const float* r) {
     store_lane<OT, E>(out + (b0 + bag) * p.out_row_stride, r);
   });
 }
@@ -875,9 +852,9 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
   const int fi = tile / p.tiles_per_field;
   if constexpr (FORM != kTileRanked) {
     using Stream = StreamShape<TT, LANES, VPL>;
-    static_assert(BUF && Stream::ok, "streamed tiles need buffer loads and 256 B - 1 KiB rows");
+    static_assert(BUF && Stream::ok, "streamed tiles need buffer loads and 256-byte rows");
     using IT = typename std::conditional<FORM == kTileStream32, int32_t, int64_t>::type;
-    pool_tile_stream<TT, OT, IT, Stream::VB, Stream::K, TileShape<TT, LANES, VPL>::NB>(p, fi,
+    pool_tile_stream<TT, OT, IT, Stream::K, TileShape<TT, LANES, VPL>::NB>(p, fi,
                                                                                        tile - fi * p.tiles_per_field);
   } else {
     pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s.tile);
