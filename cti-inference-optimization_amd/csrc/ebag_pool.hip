@@ -490,14 +490,14 @@ __device__ __forceinline__ void pool_tile(const PoolParams& p, int fi, int local
 
 // ---------------------------------------------------------------------------------------------
 // Streamed tile. A tile's bags are consecutive bags of one field, so with well-formed offsets
-// their rows are one contiguous run of `values`. Here the whole wavefront walks that run in
-// order, one row per load instruction (each lane holds VB bytes of every row: row_bytes = 64 *
-// VB), keeping K row loads in flight across bag boundaries: after it adds row r it issues row
-// r + K into the same registers. A bag's sum is finished (and stored) when its last row has been
-// added, so every bag is a sequential fp32 sum in element order, whatever its length. Row ids go
-// one 64-row chunk at a time through a lane vector and are broadcast with readlane; the chunk
-// after the current one is in flight meanwhile. Returns false (and does nothing) when the
-// tile's bags are not contiguous; the caller then pools the tile with pool_tile.
+// their rows are one contiguous run of `values`. Here the whole wavefront walks the tile's rows in
+// order, one 256-byte row per load instruction (each lane holds 4 bytes of every row), keeping K
+// row loads in flight across bag boundaries: after it adds row r it issues row r + K into the
+// same registers. A bag's sum is finished (and stored) when its last row has been added, so every
+// bag is a sequential fp32 sum in element order, whatever its length. Row ids go one 64-row chunk
+// at a time through a lane vector and are broadcast with readlane; the chunk after the current
+// one is in flight meanwhile. Bags that are not one run (malformed offsets) are walked the same
+// way, walk rows mapped to `values` positions by a search over the bags' ends.
 // ---------------------------------------------------------------------------------------------
 // The elements of a row that one 32-bit word holds (one fp32, or two bf16 / fp16), added in
 // element order.
