@@ -735,6 +735,9 @@ def main():
                     help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
                          "step end to end from host batches")
     ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
+    ap.add_argument("--index-dtype", choices=["int64", "int32"], default="int64",
+                    help="ids as the kernel reads them: int64 as the reference's collate produces them (default), "
+                         "or int32 as InputStager delivers them to the device")
     ap.add_argument("--legs", default="pool,fused,int8,addressing",
                     help="--stage reference: which of pool, fused, int8, addressing to time")
     ap.add_argument("--dispatch-order", choices=["auto", "host", "launch", "off"], default="auto",
@@ -789,7 +792,8 @@ def main():
         return bench_encoder(args, pkg, wls, dev)
     log("filling tables on the device")
     tables = W.make_tables(wl0, dev, seed=0)
-    inputs = [W.to_device(wl, dev) for wl in wls]
+    idx_dtype = torch.int32 if args.index_dtype == "int32" else torch.int64
+    inputs = [W.to_device(wl, dev, index_dtype=idx_dtype) for wl in wls]
     pooled_tables = tables
     if args.int8:
         log("quantising the tables to int8")
@@ -807,8 +811,9 @@ def main():
     out = torch.empty((wl0.batch, sum(wl0.dims)), dtype=wl0.out_dtype, device=dev)
     if args.stage == "layernorm":
         return bench_layernorm(args, pkg, plan, inputs, wl0, dev)
-    bytes_alg = [wl.bytes_algorithmic(int8=args.int8) for wl in wls]
-    bytes_comp = [wl.bytes_compulsory(int8=args.int8) for wl in wls]
+    ib = 4 if args.index_dtype == "int32" else 8
+    bytes_alg = [wl.bytes_algorithmic(int8=args.int8, index_bytes=ib) for wl in wls]
+    bytes_comp = [wl.bytes_compulsory(int8=args.int8, index_bytes=ib) for wl in wls]
     torch.cuda.synchronize()
 
     def step(i):
@@ -894,8 +899,10 @@ def main():
                    "fields": wl0.num_fields, "dims": sorted(set(wl0.dims)), "pooling": wl0.pooling,
                    "nnz_mean": float(np.mean([wl.nnz for wl in wls])), "index_sets": args.sets,
                    "length_binning": bool(args.bins), "int8_tables": bool(args.int8),
-                   "dispatch_order": args.dispatch_order},
+                   "dispatch_order": args.dispatch_order, "index_dtype": args.index_dtype},
+        # the profiles' counters were taken with int64 ids: int32 launches report no traffic
         "roofline": roofline(achieved, used_bytes, mean_launch_s, kernel_name,
+                             None if args.index_dtype == "int32" else
                              (args.workload + ("-int8" if args.int8 else ""), prof_kernel,
                               {"host": ("hbm_bytes_per_launch",),
                                "launch": ("hbm_bytes_per_launch_order_launch", "hbm_bytes_per_launch"),

@@ -66,17 +66,19 @@ class Workload:
     def lengths(self) -> np.ndarray:
         return np.diff(self.offsets)
 
-    def bytes_algorithmic(self, int8: bool = False) -> int:
+    def bytes_algorithmic(self, int8: bool = False, index_bytes: int = 0) -> int:
         """Each lookup's row once, plus indices, offsets and the output (logical bytes).
-        With ``int8`` the rows are int8 row-quantised: 1 byte per element + a 4-byte scale."""
+        With ``int8`` the rows are int8 row-quantised: 1 byte per element + a 4-byte scale.
+        ``index_bytes``: bytes per id as the kernel reads them (0: the generated int64)."""
         tb = 1 if int8 else torch.tensor([], dtype=self.table_dtype).element_size()
         extra = 4 if int8 else 0
         ob = torch.tensor([], dtype=self.out_dtype).element_size()
         L = self.lengths().reshape(self.num_fields, self.batch).sum(axis=1)
         rows = int(sum(int(L[f]) * (self.dims[f] * tb + extra) for f in range(self.num_fields)))
-        return rows + self.nnz * self.values.itemsize + self.offsets.size * 8 + self.batch * sum(self.dims) * ob
+        ib = index_bytes or self.values.itemsize
+        return rows + self.nnz * ib + self.offsets.size * 8 + self.batch * sum(self.dims) * ob
 
-    def bytes_compulsory(self, int8: bool = False) -> int:
+    def bytes_compulsory(self, int8: bool = False, index_bytes: int = 0) -> int:
         """As bytes_algorithmic, but each distinct (field, row) read once."""
         tb = 1 if int8 else torch.tensor([], dtype=self.table_dtype).element_size()
         extra = 4 if int8 else 0
@@ -86,7 +88,8 @@ class Workload:
             s, e = int(self.offsets[f * self.batch]), int(self.offsets[(f + 1) * self.batch])
             rows = np.clip(self.values[s:e], 0, self.vocab[f] - 1)
             total += np.unique(rows).size * (self.dims[f] * tb + extra)
-        return total + self.nnz * self.values.itemsize + self.offsets.size * 8 + self.batch * sum(self.dims) * ob
+        ib = index_bytes or self.values.itemsize
+        return total + self.nnz * ib + self.offsets.size * 8 + self.batch * sum(self.dims) * ob
 
 
 @lru_cache(maxsize=4)
