@@ -130,3 +130,56 @@ def test_explicit_short_bag_limit_takes_the_ranked_tiles(pkg, dev):
     split = pooled(pkg, dev, *args, long_threshold=-1)
     assert not np.array_equal(split, want)  # the split sums round differently somewhere
     np.testing.assert_allclose(split, want, rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("tdt,D", [("bf16", 128), ("f32", 64)])
+@pytest.mark.parametrize("odt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_special_values_streamed(pkg, dev, tdt, D, odt, pooling):
+    """Inf, NaN, overflow, subnormals, signed zeros and bf16 / fp16 rounding ties in bags of one,
+    two and three rows, through the streamed walk: finite and infinite results bit for bit, NaN
+    where the oracle has NaN."""
+    from test_gpu_parity import _special_rows
+    table32 = _special_rows(D)
+    table = orc.encode(table32, tdt)
+    n = len(table32)
+    bags = [[i] for i in range(n)] + [[i, j] for i in range(n) for j in range(n)] + \
+           [[i, j, k] for i in range(0, n, 3) for j in range(1, n, 4) for k in range(2, n, 5)]
+    np.random.default_rng(6).shuffle(bags)
+    lens = np.array([len(x) for x in bags])
+    values = np.concatenate([np.array(x, np.int64) for x in bags])
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    got = pooled(pkg, dev, values, offsets, [table], tdt, pooling, odt)
+    ref = orc.pool_c(values, offsets, [table], tdt, pooling, odt)
+    g, r = orc.decode(got, odt), orc.decode(ref, odt)
+    assert np.array_equal(np.isnan(g), np.isnan(r))
+    fin = ~np.isnan(r)
+    assert np.array_equal(got[fin], ref[fin])
+
+
+def test_walks_ending_at_step_and_chunk_edges(pkg, dev):
+    """Tiles (8 consecutive bags) whose rows number exactly a multiple of the 16-row step or of the
+    64-row id chunk, one more or one less, with the rows in one bag or spread over all eight, and
+    bags ending on the last row of a step."""
+    rng = np.random.default_rng(21)
+    V, D = 3000, 128
+    tiles = []
+    for T in (1, 15, 16, 17, 31, 32, 48, 63, 64, 65, 80, 127, 128, 129, 192, 256):
+        tiles.append([T] + [0] * 7)                      # one bag holds the walk
+        tiles.append([0] * 7 + [T])                      # the last bag holds it, after seven empty ones
+        cuts = np.sort(rng.integers(0, T + 1, 7))
+        tiles.append(list(np.diff(np.concatenate([[0], cuts, [T]]))))  # spread over all eight
+    tiles.append([16] * 8)                               # every bag ends on a step's last row
+    tiles.append([64, 0, 64, 0, 1, 63, 0, 0])
+    L = np.array([x for t in tiles for x in t], np.int64)
+    B = L.size  # one field, tiles in order
+    ids = make_ids(rng, int(L.sum()), V)
+    offsets = np.concatenate([[0], np.cumsum(L)]).astype(np.int64)
+    table = make_table(rng, V, D, "bf16")
+    for pooling in ("sum", "mean"):
+        want = orc.pool_c(ids, offsets, [table], "bf16", pooling, "f32")
+        assert np.array_equal(pooled(pkg, dev, ids, offsets, [table], "bf16", pooling, "f32"), want), pooling
+        narrow = np.clip(ids, -2 ** 31, 2 ** 31 - 1).astype(np.int32)
+        want32 = orc.pool_c(narrow, offsets, [table], "bf16", pooling, "f32")
+        got32 = pooled(pkg, dev, narrow, offsets, [table], "bf16", pooling, "f32", idx=torch.int32)
+        assert np.array_equal(got32, want32), pooling
