@@ -592,3 +592,16 @@ def test_hetero_binned_full_size_integer_tables_bitwise(pkg, dev):
         col += wl.dims[f]
     del tables
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("tdt,D", [("bf16", 512), ("f32", 256)])
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_one_lane_group_rows_are_sequential(pkg, dev, tdt, D, pooling):
+    """1 KiB rows fill a wavefront with one lane group, so a bag above the short-bag limit is
+    still walked in element order by that group: every bag, up to 300 rows, equals the oracle's
+    sequential sum bit for bit (the reference's own [5M, 512] table has these rows)."""
+    case = random_case(D + len(pooling), F=3, B=21, dims=(D,), V=(800,), max_len=40, tdt=tdt,
+                       long_every=4, long_len=300)
+    want = orc.pool_c(case.values, case.offsets, case.tables, tdt, pooling, tdt)
+    got = gpu_pool(pkg, dev, case.values, case.offsets, case.tables, tdt, pooling, tdt)
+    assert np.array_equal(got, want)
