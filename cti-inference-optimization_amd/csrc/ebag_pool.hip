@@ -235,12 +235,25 @@ __device__ __forceinline__ int64_t load_offset(const PoolParams& p, const void* 
   return p.off32 ? static_cast<int64_t>(static_cast<const int32_t*>(a)[i]) : static_cast<const int64_t*>(a)[i];
 }
 
+// Bag b of field gidx: values[start, end), clamped to [0, nnz]. The three loads are issued before
+// any is used (a branch around the optional base, or a conversion right after each load, would
+// make each wait for the one before): without val_base the base is read from the offsets array
+// and masked off.
+template <typename OFF>
+__device__ __forceinline__ void bag_range_typed(const PoolParams& p, int gidx, int64_t b, int64_t& start,
+                                                int64_t& end) {
+  const int64_t i = static_cast<int64_t>(gidx) * p.offsets_stride + b;
+  const OFF* const o = static_cast<const OFF*>(p.offsets);
+  const OFF* const vb = p.val_base ? static_cast<const OFF*>(p.val_base) + gidx : o;
+  const OFF x0 = o[i], x1 = o[i + 1], xb = *vb;
+  const int64_t base = p.val_base ? static_cast<int64_t>(xb) : 0;
+  start = clamp_i64(base + static_cast<int64_t>(x0), 0, p.nnz);
+  end = clamp_i64(base + static_cast<int64_t>(x1), start, p.nnz);
+}
 __device__ __forceinline__ void bag_range(const PoolParams& p, int gidx, int64_t b,
                                           int64_t& start, int64_t& end) {
-  const int64_t i = static_cast<int64_t>(gidx) * p.offsets_stride + b;
-  const int64_t base = p.val_base ? load_offset(p, p.val_base, gidx) : 0;
-  start = clamp_i64(base + load_offset(p, p.offsets, i), 0, p.nnz);
-  end = clamp_i64(base + load_offset(p, p.offsets, i + 1), start, p.nnz);
+  if (p.off32) bag_range_typed<int32_t>(p, gidx, b, start, end);
+  else bag_range_typed<int64_t>(p, gidx, b, start, end);
 }
 
 // Row shape of one kernel instance.
