@@ -678,12 +678,15 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
       load_chunk(raw_next, j + K + kWave);
     }
     if (j + K <= T) {
+      unsigned int roff[K];  // this step's row offsets, uniform (scalar registers)
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        roff[k] = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k)) << shift;
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         acc_word<TT>(acc, v[k]);
         if (j + k + 1 == next_end) flush(j + k + 1);
-        const unsigned int r = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k));
-        v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, (r << shift) + lane_off, 0, 0);
+        v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, roff[k] + lane_off, 0, 0);
       }
     } else {
 #pragma unroll
