@@ -1,6 +1,7 @@
 // Device helpers shared by the embedding-bag kernels (gfx950, wave64).
 #pragma once
 
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
@@ -122,20 +123,64 @@ __device__ __forceinline__ void acc_row(float* a, const uint4& v, float s) {
   else acc16(a, v, TT{});
 }
 
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Output blocks of at least this many bytes are stored non-temporally (`stream`: through L2 with
+// evict-first priority). A block that large would not stay in the caches until its consumer reads
+// it, and streaming it keeps the table rows that later lookups hit in L2 (lazy-32k's 235 MB block:
+// pooling 280 -> 269 us, pooling then LayerNorm 441 -> 433.5 us). A smaller block is stored plainly
+// and stays in the 256 MB memory-side cache for its consumer (bf16-2m's 29 MB block streamed:
+// pooling 0.8 us faster, the LayerNorm that reads it 2.7 us slower).
+constexpr int64_t kStreamOutBytes = int64_t{128} << 20;
+
+template <bool STREAM, typename V>
+__device__ __forceinline__ void put_as(V* dst, V v) {
+  if constexpr (STREAM) __builtin_nontemporal_store(v, dst);
+  else *dst = v;
+}
+template <typename V>
+__device__ __forceinline__ void put(V* dst, V v, bool stream) {
+  if (stream) {
+    // the barriers keep the two stores apart: hoisted or sunk into one, the store would lose its
+    // non-temporal hint
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_nontemporal_store(v, dst);
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+    *dst = v;
+  }
+}
+// Runs f(std::true_type) when `stream` (uniform) is set, else f(std::false_type): a loop of stores
+// written as f then holds no branch per store. The barriers keep the two copies apart (as in put).
+template <typename F>
+__device__ __forceinline__ void with_stream(bool stream, F&& f) {
+  if (stream) {
+    __builtin_amdgcn_sched_barrier(0);
+    f(std::true_type{});
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+    f(std::false_type{});
+  }
+}
+__device__ __forceinline__ void put4(void* dst, uint32_t x, uint32_t y, uint32_t z, uint32_t w, bool stream) {
+  const u32x4 v = {x, y, z, w};
+  put(reinterpret_cast<u32x4*>(dst), v, stream);
+}
+__device__ __forceinline__ void put2(void* dst, uint32_t x, uint32_t y, bool stream) {
+  const u32x2 v = {x, y};
+  put(reinterpret_cast<u32x2*>(dst), v, stream);
+}
+
 // Store N fp32 values as output type OT (N * sizeof(OT) is a multiple of 8 bytes and the
 // destination is aligned to that size by the host-side variant selection).
 template <int N>
-__device__ __forceinline__ void store_out(float* dst, const float* a) {
+__device__ __forceinline__ void store_out(float* dst, const float* a, bool stream) {
   static_assert(N % 4 == 0, "fp32 stores are 16-byte vectors");
 #pragma unroll
-  for (int i = 0; i < N; i += 4) {
-    uint4 v;
-    v.x = __float_as_uint(a[i]);
-    v.y = __float_as_uint(a[i + 1]);
-    v.z = __float_as_uint(a[i + 2]);
-    v.w = __float_as_uint(a[i + 3]);
-    *reinterpret_cast<uint4*>(dst + i) = v;
-  }
+  for (int i = 0; i < N; i += 4)
+    put4(dst + i, __float_as_uint(a[i]), __float_as_uint(a[i + 1]), __float_as_uint(a[i + 2]),
+         __float_as_uint(a[i + 3]), stream);
 }
 // Two fp32 values to a packed bf16 pair, IEEE round to nearest even (one v_cvt_pk_bf16_f32 on
 // gfx950): +-Inf and values that round past the largest finite bf16 become +-Inf, NaN stays NaN.
@@ -147,58 +192,42 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 template <int N>
-__device__ __forceinline__ void store_out(bf16_t* dst, const float* a) {
+__device__ __forceinline__ void store_out(bf16_t* dst, const float* a, bool stream) {
   static_assert(N % 4 == 0, "16-bit stores are 8- or 16-byte vectors");
   if constexpr (N % 8 == 0) {
 #pragma unroll
-    for (int i = 0; i < N; i += 8) {
-      uint4 v;
-      v.x = pack_bf16x2(a[i], a[i + 1]);
-      v.y = pack_bf16x2(a[i + 2], a[i + 3]);
-      v.z = pack_bf16x2(a[i + 4], a[i + 5]);
-      v.w = pack_bf16x2(a[i + 6], a[i + 7]);
-      *reinterpret_cast<uint4*>(dst + i) = v;
-    }
+    for (int i = 0; i < N; i += 8)
+      put4(dst + i, pack_bf16x2(a[i], a[i + 1]), pack_bf16x2(a[i + 2], a[i + 3]), pack_bf16x2(a[i + 4], a[i + 5]),
+           pack_bf16x2(a[i + 6], a[i + 7]), stream);
   } else {
 #pragma unroll
-    for (int i = 0; i < N; i += 4) {
-      uint2 v;
-      v.x = pack_bf16x2(a[i], a[i + 1]);
-      v.y = pack_bf16x2(a[i + 2], a[i + 3]);
-      *reinterpret_cast<uint2*>(dst + i) = v;
-    }
+    for (int i = 0; i < N; i += 4)
+      put2(dst + i, pack_bf16x2(a[i], a[i + 1]), pack_bf16x2(a[i + 2], a[i + 3]), stream);
   }
 }
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+}
 template <int N>
-__device__ __forceinline__ void store_out(f16_t* dst, const float* a) {
+__device__ __forceinline__ void store_out(f16_t* dst, const float* a, bool stream) {
   static_assert(N % 4 == 0, "16-bit stores are 8- or 16-byte vectors");
   if constexpr (N % 8 == 0) {
 #pragma unroll
-    for (int i = 0; i < N; i += 8) {
-      uint4 v;
-      v.x = f32_to_f16_bits(a[i]) | (f32_to_f16_bits(a[i + 1]) << 16);
-      v.y = f32_to_f16_bits(a[i + 2]) | (f32_to_f16_bits(a[i + 3]) << 16);
-      v.z = f32_to_f16_bits(a[i + 4]) | (f32_to_f16_bits(a[i + 5]) << 16);
-      v.w = f32_to_f16_bits(a[i + 6]) | (f32_to_f16_bits(a[i + 7]) << 16);
-      *reinterpret_cast<uint4*>(dst + i) = v;
-    }
+    for (int i = 0; i < N; i += 8)
+      put4(dst + i, pack_f16x2(a[i], a[i + 1]), pack_f16x2(a[i + 2], a[i + 3]), pack_f16x2(a[i + 4], a[i + 5]),
+           pack_f16x2(a[i + 6], a[i + 7]), stream);
   } else {
 #pragma unroll
-    for (int i = 0; i < N; i += 4) {
-      uint2 v;
-      v.x = f32_to_f16_bits(a[i]) | (f32_to_f16_bits(a[i + 1]) << 16);
-      v.y = f32_to_f16_bits(a[i + 2]) | (f32_to_f16_bits(a[i + 3]) << 16);
-      *reinterpret_cast<uint2*>(dst + i) = v;
-    }
+    for (int i = 0; i < N; i += 4) put2(dst + i, pack_f16x2(a[i], a[i + 1]), pack_f16x2(a[i + 2], a[i + 3]), stream);
   }
 }
 
-__device__ __forceinline__ void store_one(float* dst, float a) { *dst = a; }
-__device__ __forceinline__ void store_one(bf16_t* dst, float a) {
-  *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(pack_bf16x2(a, 0.f));
+__device__ __forceinline__ void store_one(float* dst, float a, bool stream) { put(dst, a, stream); }
+__device__ __forceinline__ void store_one(bf16_t* dst, float a, bool stream) {
+  put(reinterpret_cast<uint16_t*>(dst), static_cast<uint16_t>(pack_bf16x2(a, 0.f)), stream);
 }
-__device__ __forceinline__ void store_one(f16_t* dst, float a) {
-  *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(f32_to_f16_bits(a));
+__device__ __forceinline__ void store_one(f16_t* dst, float a, bool stream) {
+  put(reinterpret_cast<uint16_t*>(dst), static_cast<uint16_t>(f32_to_f16_bits(a)), stream);
 }
 
 // a[i] / L for a bag of L >= 1 rows, each rounded once to fp32, given inv = 1/L rounded to fp64.

@@ -35,6 +35,7 @@ struct NormParams {
   int64_t rows;
   int64_t cols;
   float eps;
+  int32_t stream_out;  // the output is at least kStreamOutBytes: non-temporal stores
 };
 
 template <typename PT>
@@ -83,18 +84,20 @@ __global__ void __launch_bounds__(WAVES * kWave) norm_rows_kernel(const NormPara
     if (p.rstd_out) p.rstd_out[row] = rstd;
   }
   T* yr = reinterpret_cast<T*>(p.y + row * p.cols * Elem<T>::kBytes);
+  with_stream(p.stream_out, [&](auto stream) {
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int i = t + k * THREADS;
-    if (i < nvec) {
-      float gm[VEC], bt[VEC], r[VEC];
-      load_params<PT, VEC>(p.gamma, static_cast<int64_t>(i) * VEC, gm);
-      load_params<PT, VEC>(p.beta, static_cast<int64_t>(i) * VEC, bt);
+    for (int k = 0; k < K; ++k) {
+      const int i = t + k * THREADS;
+      if (i < nvec) {
+        float gm[VEC], bt[VEC], r[VEC];
+        load_params<PT, VEC>(p.gamma, static_cast<int64_t>(i) * VEC, gm);
+        load_params<PT, VEC>(p.beta, static_cast<int64_t>(i) * VEC, bt);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) r[e] = v[k][e] * rstd * gm[e] + bt[e];
-      store_out<VEC>(yr + static_cast<int64_t>(i) * VEC, r);
+        for (int e = 0; e < VEC; ++e) r[e] = v[k][e] * rstd * gm[e] + bt[e];
+        store_out<VEC>(yr + static_cast<int64_t>(i) * VEC, r, decltype(stream)::value);
+      }
     }
-  }
+  });
 }
 
 // Any width and alignment: three passes over the row (sum, squared deviations, output).
@@ -119,10 +122,12 @@ __global__ void __launch_bounds__(kNormThreads) norm_rows_loop_kernel(const Norm
     if (p.rstd_out) p.rstd_out[row] = rstd;
   }
   T* yr = reinterpret_cast<T*>(p.y + row * p.cols * Elem<T>::kBytes);
-  for (int64_t c = threadIdx.x; c < p.cols; c += kNormThreads) {
-    const float d = Elem<T>::load(xr + c * Elem<T>::kBytes) - mean;
-    store_one(yr + c, d * rstd * load_param<PT>(p.gamma, c) + load_param<PT>(p.beta, c));
-  }
+  with_stream(p.stream_out, [&](auto stream) {
+    for (int64_t c = threadIdx.x; c < p.cols; c += kNormThreads) {
+      const float d = Elem<T>::load(xr + c * Elem<T>::kBytes) - mean;
+      store_one(yr + c, d * rstd * load_param<PT>(p.gamma, c) + load_param<PT>(p.beta, c), decltype(stream)::value);
+    }
+  });
 }
 
 template <typename T, typename PT>
@@ -187,6 +192,7 @@ extern "C" int cti_ebag_layernorm(const void* x, void* y, int64_t rows, int64_t 
   p.rows = rows;
   p.cols = cols;
   p.eps = eps;
+  p.stream_out = rows * cols * dtype_bytes(dtype) >= kStreamOutBytes;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   switch (dtype) {

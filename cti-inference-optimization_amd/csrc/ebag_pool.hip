@@ -154,6 +154,7 @@ struct PoolParams {
                             // reference's int8 kernel stores acc.to(bfloat16), online_best/infer.py:941)
   int32_t stream_ok;        // 256-byte rows may take streamed tiles (no binning, default short-bag
                             // limit, walks and id offsets within 32 bits)
+  int32_t stream_out;       // the output block is at least kStreamOutBytes: non-temporal stores
   FieldDesc f[kMaxFields];
 };
 
@@ -326,7 +327,7 @@ __device__ __forceinline__ void store_bag(const PoolParams& p, int64_t b, int ou
   round_like_reference<TT, S::NACC>(p, r);
   OT* o = reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col;
 #pragma unroll
-  for (int q = 0; q < VPL; ++q) store_out<S::VEC>(o + (q * LANES + sl) * S::VEC, r + q * S::VEC);
+  for (int q = 0; q < VPL; ++q) store_out<S::VEC>(o + (q * LANES + sl) * S::VEC, r + q * S::VEC, p.stream_out);
 }
 
 // U row loads of one step: elements k .. k+U-1 of this subgroup's current chunk, whose row ids
@@ -527,20 +528,24 @@ __device__ __forceinline__ void acc_word(float* a, uint32_t w) {
   }
 }
 
-// E = 1 or 2 output elements of one lane (aligned to E * sizeof(OT) bytes).
-template <typename OT, int E>
+// E = 1 or 2 output elements of one lane (aligned to E * sizeof(OT) bytes); STREAM: non-temporal.
+template <typename OT, int E, bool STREAM>
 __device__ __forceinline__ void store_lane(OT* dst, const float* a) {
   if constexpr (E == 1) {
-    store_one(dst, a[0]);
+    if constexpr (sizeof(OT) == 4) put_as<STREAM>(reinterpret_cast<float*>(dst), a[0]);
+    else if constexpr (__is_same(OT, bf16_t))
+      put_as<STREAM>(reinterpret_cast<uint16_t*>(dst), static_cast<uint16_t>(pack_bf16x2(a[0], 0.f)));
+    else put_as<STREAM>(reinterpret_cast<uint16_t*>(dst), static_cast<uint16_t>(f32_to_f16_bits(a[0])));
   } else if constexpr (sizeof(OT) == 4) {
     static_assert(E == 2, "two fp32 values");
-    *reinterpret_cast<uint2*>(dst) = make_uint2(__float_as_uint(a[0]), __float_as_uint(a[1]));
+    const u32x2 v = {__float_as_uint(a[0]), __float_as_uint(a[1])};
+    put_as<STREAM>(reinterpret_cast<u32x2*>(dst), v);
   } else if constexpr (__is_same(OT, bf16_t)) {
     static_assert(E == 2, "two 16-bit values");
-    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(a[0], a[1]);
+    put_as<STREAM>(reinterpret_cast<uint32_t*>(dst), pack_bf16x2(a[0], a[1]));
   } else {
     static_assert(E == 2, "two 16-bit values");
-    *reinterpret_cast<uint32_t*>(dst) = f32_to_f16_bits(a[0]) | (f32_to_f16_bits(a[1]) << 16);
+    put_as<STREAM>(reinterpret_cast<uint32_t*>(dst), pack_f16x2(a[0], a[1]));
   }
 }
 
@@ -700,8 +705,9 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
   }
 }
 
-// A tile of NB consecutive bags of one field, streamed (see stream_walk).
-template <typename TT, typename OT, typename IT, int K, int NB>
+// A tile of NB consecutive bags of one field, streamed (see stream_walk); STREAM_OUT: the results
+// are stored non-temporally (the host sets it for output blocks of kStreamOutBytes and more).
+template <typename TT, typename OT, typename IT, int K, int NB, bool STREAM_OUT>
 __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, int local_tile) {
   constexpr int E = 4 / Elem<TT>::kBytes;
   const int lane = lane_id();
@@ -714,7 +720,7 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
       static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(p.f[fi].row_bytes)));
   OT* const out = reinterpret_cast<OT*>(p.out) + p.f[fi].out_col + lane * E;
   stream_walk<TT, IT, K, NB>(p, rsrc, shift, p.f[fi].max_row, nb, start, end, [&](int bag, const float* r) {
-    store_lane<OT, E>(out + (b0 + bag) * p.out_row_stride, r);
+    store_lane<OT, E, STREAM_OUT>(out + (b0 + bag) * p.out_row_stride, r);
   });
 }
 
@@ -846,8 +852,9 @@ __device__ void order_next(const PoolParams& p, int x, int chunk, OrderLds& s) {
 
 // Main kernel: one wavefront per workgroup, one tile per workgroup (after the order workgroups,
 // when the launch makes the next batch's order).
-// Main kernel forms: tiles pooled by pool_tile, or streamed with int32 / int64 ids.
-enum TileForm : int { kTileRanked = 0, kTileStream32 = 1, kTileStream64 = 2 };
+// Main kernel forms: tiles pooled by pool_tile, or streamed with int32 / int64 ids, the results
+// stored plainly or (the Nt forms) non-temporally.
+enum TileForm : int { kTileRanked = 0, kTileStream32 = 1, kTileStream64 = 2, kTileStream32Nt = 3, kTileStream64Nt = 4 };
 
 template <typename TT, typename OT, int LANES, int VPL, bool BUF, int FORM>
 __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) {
@@ -869,9 +876,9 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
   if constexpr (FORM != kTileRanked) {
     using Stream = StreamShape<TT, LANES, VPL>;
     static_assert(BUF && Stream::ok, "streamed tiles need buffer loads and 256-byte rows");
-    using IT = typename std::conditional<FORM == kTileStream32, int32_t, int64_t>::type;
-    pool_tile_stream<TT, OT, IT, Stream::K, TileShape<TT, LANES, VPL>::NB>(p, fi,
-                                                                                       tile - fi * p.tiles_per_field);
+    using IT = typename std::conditional<FORM == kTileStream32 || FORM == kTileStream32Nt, int32_t, int64_t>::type;
+    constexpr bool kNt = FORM == kTileStream32Nt || FORM == kTileStream64Nt;
+    pool_tile_stream<TT, OT, IT, Stream::K, TileShape<TT, LANES, VPL>::NB, kNt>(p, fi, tile - fi * p.tiles_per_field);
   } else {
     pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s.tile);
   }
@@ -1009,7 +1016,7 @@ __global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p
     for (int i = 0; i < S::NACC; ++i) r[i] = a[i];
     if (p.pooling == CTI_EBAG_MEAN && Lb > 0)
       div_by_count<S::NACC>(r, 1.0 / static_cast<double>(Lb), static_cast<float>(Lb));
-    store_out<S::VEC>(row + static_cast<int64_t>(bag) * D + sl * S::VEC, r);
+    store_out<S::VEC>(row + static_cast<int64_t>(bag) * D + sl * S::VEC, r, false);  // LDS row
   };
 
   for (int r0 = 0; r0 < n_short; r0 += R) {
@@ -1108,20 +1115,23 @@ __global__ void __launch_bounds__(W * kWave) pool_norm_kernel(const PoolParams p
   block_sum_n<W, SPW>(rstd, s_red);
 #pragma unroll
   for (int j = 0; j < SPW; ++j) rstd[j] = 1.0f / __builtin_sqrtf(rstd[j] / n + fn.eps);
-  for (int i = t; i < nvec; i += THREADS) {
-    float gm[VEC], bt[VEC];
-    load_params<PT, VEC>(fn.gamma, static_cast<int64_t>(i) * VEC, gm);
-    load_params<PT, VEC>(fn.beta, static_cast<int64_t>(i) * VEC, bt);
+  with_stream(p.stream_out, [&](auto stream) {
+    for (int i = t; i < nvec; i += THREADS) {
+      float gm[VEC], bt[VEC];
+      load_params<PT, VEC>(fn.gamma, static_cast<int64_t>(i) * VEC, gm);
+      load_params<PT, VEC>(fn.beta, static_cast<int64_t>(i) * VEC, bt);
 #pragma unroll
-    for (int j = 0; j < SPW; ++j) {
-      if (b0 + j >= p.batch) break;
-      float x[VEC], r[VEC];
-      unpack16(load16(rb + j * rstride + i * 16), x, TT{});
+      for (int j = 0; j < SPW; ++j) {
+        if (b0 + j >= p.batch) break;
+        float x[VEC], r[VEC];
+        unpack16(load16(rb + j * rstride + i * 16), x, TT{});
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) r[e] = (x[e] - mean[j]) * rstd[j] * gm[e] + bt[e];
-      store_out<VEC>(reinterpret_cast<TT*>(p.out) + (b0 + j) * p.out_row_stride + static_cast<int64_t>(i) * VEC, r);
+        for (int e = 0; e < VEC; ++e) r[e] = (x[e] - mean[j]) * rstd[j] * gm[e] + bt[e];
+        store_out<VEC>(reinterpret_cast<TT*>(p.out) + (b0 + j) * p.out_row_stride + static_cast<int64_t>(i) * VEC, r,
+                       decltype(stream)::value);
+      }
     }
-  }
+  });
 }
 
 // Length-binning pass: list the bags longer than block_threshold, those longer than
@@ -1306,7 +1316,7 @@ __device__ __forceinline__ void store_bag_rt(const PoolParams& p, int64_t b, int
   for (int i = 0; i < VEC; ++i) r[i] = a[i];
   if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<VEC>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
   round_like_reference<TT, VEC>(p, r);
-  store_out<VEC>(reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col + sl * VEC, r);
+  store_out<VEC>(reinterpret_cast<OT*>(p.out) + b * p.out_row_stride + out_col + sl * VEC, r, p.stream_out);
 }
 
 // ... or, in a mixed launch, each field's own (one lane vector per lane, 1 << lanes_log2 lanes
@@ -1470,7 +1480,7 @@ __global__ void __launch_bounds__(kMainThreads) pool_generic_kernel(const PoolPa
         float r = acc[i];
         if (p.pooling == CTI_EBAG_MEAN && L > 0) r = r / static_cast<float>(L);
         round_like_reference<TT, 1>(p, &r);
-        store_one(o + col, r);
+        store_one(o + col, r, p.stream_out);
       }
     }
   }
@@ -1548,8 +1558,12 @@ void launch_shape(const PoolParams& p, const LongList* l, hipStream_t s) {
       block(kMainThreads);
   constexpr bool kStream = StreamShape<TT, LANES, VPL>::ok;
   const bool stream = kStream && p.stream_ok && p.buffer_ok;
-  if (stream && p.idx32)
+  if (stream && p.idx32 && p.stream_out)
+    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true, kStream ? kTileStream32Nt : kTileRanked>), grid, block, 0, s, p);
+  else if (stream && p.idx32)
     hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true, kStream ? kTileStream32 : kTileRanked>), grid, block, 0, s, p);
+  else if (stream && p.stream_out)
+    hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true, kStream ? kTileStream64Nt : kTileRanked>), grid, block, 0, s, p);
   else if (stream)
     hipLaunchKernelGGL((pool_kernel<TT, OT, LANES, VPL, true, kStream ? kTileStream64 : kTileRanked>), grid, block, 0, s, p);
   else if (p.buffer_ok)
@@ -1761,6 +1775,7 @@ int run_job(const Job& j, hipStream_t stream) {
       p.round_bf16 = j.round_bf16;
       const bool bins = j.use_bins && v != kVarGeneric;
       p.stream_ok = stream_variant_allowed(j) ? 1 : 0;
+      p.stream_out = j.batch * j.out_row_stride * dtype_bytes(j.odt) >= kStreamOutBytes;
       if (v == kVarGeneric) p.sub_threshold = kNoLimit;
       else if (j.sub_threshold == 0) p.sub_threshold = default_sub_threshold(v, bins);
       else p.sub_threshold = j.sub_threshold < 0 ? 0 : j.sub_threshold;
@@ -1996,6 +2011,7 @@ extern "C" int cti_ebag_fused_all_slots_layernorm(const void* values, int32_t in
   p.batch = batch_size;
   p.pooling = pooling;
   p.num_fields = num_slots;
+  p.stream_out = batch_size * p.out_row_stride * tb >= kStreamOutBytes;
   p.sub_threshold = kFusedSubThreshold;
   p.block_threshold = kNoLimit;
   p.split_threshold = kNoLimit;
