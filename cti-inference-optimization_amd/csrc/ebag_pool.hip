@@ -643,13 +643,13 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
   RawIds<IT> raw, raw_next;
   load_chunk(raw, 0);
   load_chunk(raw_next, kWave);
-  unsigned int ids = lane < T ? static_cast<unsigned int>(clamp_i64(raw.value(), 0, max_row)) : r_pad;
+  unsigned int ids = (lane < T ? static_cast<unsigned int>(clamp_i64(raw.value(), 0, max_row)) : r_pad) << shift;
 
   uint32_t v[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const unsigned int r = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), k));
-    v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, (r << shift) + lane_off, 0, 0);
+    v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, r + lane_off, 0, 0);
   }
 
   float acc[E];
@@ -679,18 +679,22 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
     const int c_issue = (j + K) & (kWave - 1);  // lane of walk row j + K in its id chunk
     if (c_issue == 0) {
       // rows j + K .. are in the next chunk: take it, and load the one after it
-      ids = j + K + lane < T ? static_cast<unsigned int>(clamp_i64(raw_next.value(), 0, max_row)) : r_pad;
+      ids = (j + K + lane < T ? static_cast<unsigned int>(clamp_i64(raw_next.value(), 0, max_row)) : r_pad) << shift;
       load_chunk(raw_next, j + K + kWave);
     }
+    int dn = next_end - j - 1;  // step row after which the next bag ends
     if (j + K <= T) {
       unsigned int roff[K];  // this step's row offsets, uniform (scalar registers)
 #pragma unroll
       for (int k = 0; k < K; ++k)
-        roff[k] = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k)) << shift;
+        roff[k] = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k));
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         acc_word<TT>(acc, v[k]);
-        if (j + k + 1 == next_end) flush(j + k + 1);
+        if (k == dn) {
+          flush(j + k + 1);
+          dn = next_end - j - 1;
+        }
         v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, roff[k] + lane_off, 0, 0);
       }
     } else {
@@ -698,7 +702,10 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
       for (int k = 0; k < K; ++k) {
         if (j + k < T) {
           acc_word<TT>(acc, v[k]);
-          if (j + k + 1 == next_end) flush(j + k + 1);
+          if (k == dn) {
+            flush(j + k + 1);
+            dn = next_end - j - 1;
+          }
         }
       }
     }
@@ -718,9 +725,11 @@ __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, in
   const Rsrc rsrc = make_rsrc(p.f[fi].table, p.f[fi].span_bytes);
   const unsigned int shift =
       static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(p.f[fi].row_bytes)));
-  OT* const out = reinterpret_cast<OT*>(p.out) + p.f[fi].out_col + lane * E;
-  stream_walk<TT, IT, K, NB>(p, rsrc, shift, p.f[fi].max_row, nb, start, end, [&](int bag, const float* r) {
-    store_lane<OT, E, STREAM_OUT>(out + (b0 + bag) * p.out_row_stride, r);
+  // bags are stored in order, each once: the destination advances by one output row per bag
+  OT* dst = reinterpret_cast<OT*>(p.out) + b0 * p.out_row_stride + p.f[fi].out_col + lane * E;
+  stream_walk<TT, IT, K, NB>(p, rsrc, shift, p.f[fi].max_row, nb, start, end, [&](int, const float* r) {
+    store_lane<OT, E, STREAM_OUT>(dst, r);
+    dst += p.out_row_stride;
   });
 }
 
