@@ -675,7 +675,11 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
   };
   if (next_end == 0) flush(0);
 
-  for (int j = 0; j < T; j += K) {
+  // Full steps: rows j .. j + K - 1 are added and rows j + K .. j + 2K - 1 issued (past the walk:
+  // pad offsets, no request). The partial last step is outside the loop, so the loop carries the
+  // row window in place (no register copies, which would wait for every load in flight).
+  int j = 0;
+  for (; j + K <= T; j += K) {
     const int c_issue = (j + K) & (kWave - 1);  // lane of walk row j + K in its id chunk
     if (c_issue == 0) {
       // rows j + K .. are in the next chunk: take it, and load the one after it
@@ -683,29 +687,29 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
       load_chunk(raw_next, j + K + kWave);
     }
     int dn = next_end - j - 1;  // step row after which the next bag ends
-    if (j + K <= T) {
-      unsigned int roff[K];  // this step's row offsets, uniform (scalar registers)
+    unsigned int roff[K];       // this step's row offsets, uniform (scalar registers)
 #pragma unroll
-      for (int k = 0; k < K; ++k)
-        roff[k] = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k));
+    for (int k = 0; k < K; ++k)
+      roff[k] = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k));
 #pragma unroll
-      for (int k = 0; k < K; ++k) {
+    for (int k = 0; k < K; ++k) {
+      acc_word<TT>(acc, v[k]);
+      if (k == dn) {
+        flush(j + k + 1);
+        dn = next_end - j - 1;
+      }
+      v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, roff[k] + lane_off, 0, 0);
+    }
+  }
+  if (j < T) {  // the partial last step: rows j .. T - 1, nothing issued
+    int dn = next_end - j - 1;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (j + k < T) {
         acc_word<TT>(acc, v[k]);
         if (k == dn) {
           flush(j + k + 1);
           dn = next_end - j - 1;
-        }
-        v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, roff[k] + lane_off, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        if (j + k < T) {
-          acc_word<TT>(acc, v[k]);
-          if (k == dn) {
-            flush(j + k + 1);
-            dn = next_end - j - 1;
-          }
         }
       }
     }
