@@ -146,6 +146,7 @@ struct PoolParams {
   int32_t num_fields;
   int32_t num_tiles;
   int32_t tiles_per_field;  // every field of a launch has the same number of tiles
+  uint32_t tpf_inv;         // floor((2^32 - 1) / tiles_per_field): field_of_tile's multiplier
   int32_t pooling;          // CTI_EBAG_SUM / CTI_EBAG_MEAN
   int32_t idx32;
   int32_t off32;            // offsets and val_base are int32 (else int64)
@@ -782,12 +783,21 @@ __device__ __forceinline__ int ordered_tile(const PoolParams& p, int pos) {
   return n == p.num_tiles && magic == kOrderMagic && t >= 0 && t < p.num_tiles ? t : pos;
 }
 
+// tile / tiles_per_field for 0 <= tile < 2^31 without a division: hi32(tile * tpf_inv) with
+// tpf_inv = floor((2^32 - 1) / d) is the quotient or one less, and one compare corrects it.
+__device__ __forceinline__ int field_of_tile(const PoolParams& p, int tile) {
+  const unsigned int t = static_cast<unsigned int>(tile), d = static_cast<unsigned int>(p.tiles_per_field);
+  unsigned int q = __umulhi(t, p.tpf_inv);
+  if ((q + 1u) * d <= t) ++q;
+  return static_cast<int>(q);
+}
+
 // Rows of tile t (NB consecutive bags of one field) in the next batch, from its offsets alone. A
 // launch that makes an order holds every field of its job in job order (the host checks it), so
 // field fi's offsets start at fi * offsets_stride: no dependent load of the field's index, which
 // would make each tile's offset loads wait for the previous tile's (loads complete in order).
 __device__ __forceinline__ int64_t next_tile_rows(const PoolParams& p, int t, int nb) {
-  const int fi = t / p.tiles_per_field;
+  const int fi = field_of_tile(p, t);
   const int64_t b0 = static_cast<int64_t>(t - fi * p.tiles_per_field) * nb;
   const int64_t b1 = b0 + nb < p.batch ? b0 + nb : p.batch;
   const int64_t i = static_cast<int64_t>(fi) * p.offsets_stride;
@@ -885,7 +895,7 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
     pos -= p.order_blocks;
   }
   const int tile = ordered_tile(p, xcd_position(pos, p.num_tiles));
-  const int fi = tile / p.tiles_per_field;
+  const int fi = field_of_tile(p, tile);
   if constexpr (FORM != kTileRanked) {
     using Stream = StreamShape<TT, LANES, VPL>;
     static_assert(BUF && Stream::ok, "streamed tiles need buffer loads and 256-byte rows");
@@ -1446,7 +1456,7 @@ template <typename TT, typename OT>
 __global__ void __launch_bounds__(kMainThreads) pool_generic_kernel(const PoolParams p) {
   constexpr int NC = 4;
   const int tile = block_tile();
-  const int fi = tile / p.tiles_per_field;
+  const int fi = field_of_tile(p, tile);
   const char* const table = p.f[fi].table;
   const int64_t max_row = p.f[fi].max_row;
   const int64_t row_bytes = p.f[fi].row_bytes;
@@ -1840,6 +1850,7 @@ int run_job(const Job& j, hipStream_t stream) {
       p.num_tiles = static_cast<int32_t>(tiles);
       // every field of a single-shape launch has the same number of tiles
       p.tiles_per_field = static_cast<int32_t>(tiles / static_cast<int64_t>(nf));
+      p.tpf_inv = p.tiles_per_field > 0 ? 0xffffffffu / static_cast<uint32_t>(p.tiles_per_field) : 0u;
       if (p.next_order) {  // one workgroup per chunk of each XCD range
         const int64_t per_range = (tiles + 7) / 8;
         p.order_blocks = static_cast<int32_t>(8 * ((per_range + kOrderChunk - 1) / kOrderChunk));
