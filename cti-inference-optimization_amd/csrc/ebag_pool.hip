@@ -28,10 +28,11 @@
 //     completes under the current chunk's row loads. Tables under 4 GiB with power-of-two row sizes are read with buffer
 //     loads: a row's offset is one shift-add, and rows past a bag's end use an out-of-range offset
 //     that returns zeros without a memory request (no per-row branch).
-//   * Streamed tiles (256-byte rows of fp32 / bf16 / fp16 tables, without binning and with the
-//     default short-bag limit): the same tiles, but the wavefront walks the tile's rows in order
-//     across bag boundaries (with well-formed offsets they are one contiguous run of `values`),
-//     each lane holding 4 bytes of every row, one row per load instruction, 16 rows in flight;
+//   * Streamed tiles (256-byte rows of fp32 / bf16 / fp16 tables and 128-byte rows of int8 tables,
+//     without binning and with the default short-bag limit): the same tiles, but the wavefront
+//     walks the tile's rows in order across bag boundaries (with well-formed offsets they are one
+//     contiguous run of `values`), each lane holding 4 bytes (int8: 2 bytes and the row's scale)
+//     of every row, one row per load instruction, 16 rows in flight;
 //     a bag is stored when its last row has been added, so every bag, whatever its length, is a
 //     sequential fp32 sum in element order. Row ids come one 64-row chunk at a time through
 //     buffer loads over `values` (the next chunk in flight) and are broadcast with readlane.
@@ -153,8 +154,8 @@ struct PoolParams {
   int32_t buffer_ok;        // every field's span_bytes is set: rows are read with buffer loads
   int32_t round_bf16;       // int8 tables: round each result to bf16 before the output type (the
                             // reference's int8 kernel stores acc.to(bfloat16), online_best/infer.py:941)
-  int32_t stream_ok;        // 256-byte rows may take streamed tiles (no binning, default short-bag
-                            // limit, walks and id offsets within 32 bits)
+  int32_t stream_ok;        // rows of 16 lane vectors may take streamed tiles (no binning, default
+                            // short-bag limit, walks and id offsets within 32 bits)
   int32_t stream_out;       // the output block is at least kStreamOutBytes: non-temporal stores
   FieldDesc f[kMaxFields];
 };
@@ -550,13 +551,34 @@ __device__ __forceinline__ void store_lane(OT* dst, const float* a) {
   }
 }
 
-// Streamed tiles serve 256-byte rows of fp32 / bf16 / fp16 tables read with buffer loads: a row is
-// one 4-byte word per lane.
+// Streamed tiles serve rows of 16 lane vectors read with buffer loads: 256-byte rows of fp32 / bf16
+// / fp16 tables (4 bytes per lane) and 128-byte rows of int8 tables (2 bytes per lane, each row's
+// scale read with it).
 template <typename TT, int LANES, int VPL>
 struct StreamShape {
-  static constexpr bool ok = !Quantized<TT>::value && LANES == 16 && VPL == 1;  // 256-byte rows
-  static constexpr int K = 16;  // rows in flight: 16 VGPRs of row data
+  static constexpr bool ok = LANES == 16 && VPL == 1;
+  static constexpr int BPL = LANES * Elem<TT>::kVecBytes / kWave;  // bytes of a row per lane
+  static constexpr int K = 16;  // rows in flight: 16 VGPRs of row data (and 16 of scales)
 };
+
+// The BPL bytes of one lane's part of a row (loaded zero-extended into 32 bits) into the
+// accumulators: fp32 / bf16 / fp16 as acc_word; int8 bytes as fma(q, s, acc) in element order.
+template <typename TT, int BPL>
+__device__ __forceinline__ void acc_lane(float* a, uint32_t w, float s) {
+  if constexpr (Quantized<TT>::value) {
+#pragma unroll
+    for (int k = 0; k < BPL; ++k)
+      a[k] = __builtin_fmaf(static_cast<float>(static_cast<int8_t>(w >> (8 * k))), s, a[k]);
+  } else {
+    static_assert(BPL == 4, "one 32-bit word of a 256-byte row");
+    acc_word<TT>(a, w);
+  }
+}
+template <int BPL>
+__device__ __forceinline__ uint32_t load_lane(Rsrc r, unsigned int off) {
+  if constexpr (BPL == 2) return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+  else return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
 
 // Raw ids of one 64-row chunk (one per lane), as loaded: converted only when the chunk is used,
 // so the load stays in flight meanwhile.
@@ -582,13 +604,13 @@ struct RawIds<int64_t> {
 // of bag i has been added (at once for an empty bag) it calls store(i, r) with the bag's
 // E = 4 / sizeof(TT) results of this lane (divided by the length for mean pooling), i rising.
 // Walk rows are counted in 32 bits: the bags hold fewer than 2^31 rows in all (host).
-template <typename TT, typename IT, int K, int NB, typename Store>
-__device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsigned int shift, int64_t max_row, int nb,
-                                            int64_t start, int64_t end, Store&& store) {
+template <typename TT, typename IT, int K, int NB, int BPL, typename Store>
+__device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, Rsrc srsrc, unsigned int shift,
+                                            int64_t max_row, int nb, int64_t start, int64_t end, Store&& store) {
   static_assert(kWave % K == 0 && K <= kWave, "K divides the 64-row id chunk");
   static_assert(NB <= kWave, "one lane per bag");
-  static_assert(!Quantized<TT>::value, "unquantised rows");
-  constexpr int E = 4 / Elem<TT>::kBytes;  // elements per lane and row
+  constexpr bool Q = Quantized<TT>::value;
+  constexpr int E = BPL / Elem<TT>::kBytes;  // elements per lane and row
   const int lane = lane_id();
   const bool valid = lane < nb;
   if (nb <= 0) return;
@@ -638,7 +660,10 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
   };
 
   const unsigned int r_pad = 0xffffffffu >> shift;  // offsets past the table: zeros, no request
-  const unsigned int lane_off = static_cast<unsigned int>(lane * 4);
+  const unsigned int lane_off = static_cast<unsigned int>(lane * BPL);
+  // int8 rows: a row's scale offset is its row offset >> (shift - 2) (past the scales for the pad
+  // rows, whose row offsets lie past the table: the host admits only (rows + 1) * row_bytes <= 2^32)
+  const unsigned int sshift = shift - 2;
 
   // clamped row ids of the chunk being issued; the next chunk's raw ids are in flight meanwhile
   RawIds<IT> raw, raw_next;
@@ -647,10 +672,12 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
   unsigned int ids = (lane < T ? static_cast<unsigned int>(clamp_i64(raw.value(), 0, max_row)) : r_pad) << shift;
 
   uint32_t v[K];
+  float sc[K] = {};  // int8 rows: each row's scale, loaded with it (unused otherwise)
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const unsigned int r = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), k));
-    v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, r + lane_off, 0, 0);
+    v[k] = load_lane<BPL>(rsrc, r + lane_off);
+    if constexpr (Q) sc[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, r >> sshift, 0, 0));
   }
 
   float acc[E];
@@ -666,6 +693,7 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
 #pragma unroll
       for (int i = 0; i < E; ++i) r[i] = acc[i];
       if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<E>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
+      round_like_reference<TT, E>(p, r);
       store(bag, r);
 #pragma unroll
       for (int i = 0; i < E; ++i) acc[i] = 0.f;
@@ -694,12 +722,13 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
       roff[k] = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k));
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      acc_word<TT>(acc, v[k]);
+      acc_lane<TT, BPL>(acc, v[k], sc[k]);
       if (k == dn) {
         flush(j + k + 1);
         dn = next_end - j - 1;
       }
-      v[k] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, roff[k] + lane_off, 0, 0);
+      v[k] = load_lane<BPL>(rsrc, roff[k] + lane_off);
+      if constexpr (Q) sc[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, roff[k] >> sshift, 0, 0));
     }
   }
   if (j < T) {  // the partial last step: rows j .. T - 1, nothing issued
@@ -707,7 +736,7 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       if (j + k < T) {
-        acc_word<TT>(acc, v[k]);
+        acc_lane<TT, BPL>(acc, v[k], sc[k]);
         if (k == dn) {
           flush(j + k + 1);
           dn = next_end - j - 1;
@@ -719,20 +748,22 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, unsi
 
 // A tile of NB consecutive bags of one field, streamed (see stream_walk); STREAM_OUT: the results
 // are stored non-temporally (the host sets it for output blocks of kStreamOutBytes and more).
-template <typename TT, typename OT, typename IT, int K, int NB, bool STREAM_OUT>
+template <typename TT, typename OT, typename IT, int K, int NB, int BPL, bool STREAM_OUT>
 __device__ __forceinline__ void pool_tile_stream(const PoolParams& p, int fi, int local_tile) {
-  constexpr int E = 4 / Elem<TT>::kBytes;
+  constexpr int E = BPL / Elem<TT>::kBytes;
   const int lane = lane_id();
   const int64_t b0 = static_cast<int64_t>(local_tile) * NB;
   const int nb = static_cast<int>(p.batch - b0 < NB ? p.batch - b0 : NB);
   int64_t start = 0, end = 0;
   if (lane < nb) bag_range(p, p.f[fi].gidx, b0 + lane, start, end);
   const Rsrc rsrc = make_rsrc(p.f[fi].table, p.f[fi].span_bytes);
+  const Rsrc srsrc = make_rsrc(reinterpret_cast<const char*>(p.f[fi].row_scale),
+                               Quantized<TT>::value ? static_cast<uint32_t>((p.f[fi].max_row + 1) * 4) : 0u);
   const unsigned int shift =
       static_cast<unsigned int>(__builtin_ctzll(static_cast<unsigned long long>(p.f[fi].row_bytes)));
   // bags are stored in order, each once: the destination advances by one output row per bag
   OT* dst = reinterpret_cast<OT*>(p.out) + b0 * p.out_row_stride + p.f[fi].out_col + lane * E;
-  stream_walk<TT, IT, K, NB>(p, rsrc, shift, p.f[fi].max_row, nb, start, end, [&](int, const float* r) {
+  stream_walk<TT, IT, K, NB, BPL>(p, rsrc, srsrc, shift, p.f[fi].max_row, nb, start, end, [&](int, const float* r) {
     store_lane<OT, E, STREAM_OUT>(dst, r);
     dst += p.out_row_stride;
   });
@@ -898,10 +929,11 @@ __global__ void __launch_bounds__(kMainThreads) pool_kernel(const PoolParams p) 
   const int fi = field_of_tile(p, tile);
   if constexpr (FORM != kTileRanked) {
     using Stream = StreamShape<TT, LANES, VPL>;
-    static_assert(BUF && Stream::ok, "streamed tiles need buffer loads and 256-byte rows");
+    static_assert(BUF && Stream::ok, "streamed tiles need buffer loads and rows of 16 lane vectors");
     using IT = typename std::conditional<FORM == kTileStream32 || FORM == kTileStream32Nt, int32_t, int64_t>::type;
     constexpr bool kNt = FORM == kTileStream32Nt || FORM == kTileStream64Nt;
-    pool_tile_stream<TT, OT, IT, Stream::K, TileShape<TT, LANES, VPL>::NB, kNt>(p, fi, tile - fi * p.tiles_per_field);
+    pool_tile_stream<TT, OT, IT, Stream::K, TileShape<TT, LANES, VPL>::NB, Stream::BPL, kNt>(p, fi,
+                                                                                           tile - fi * p.tiles_per_field);
   } else {
     pool_tile<TT, OT, LANES, VPL, BUF>(p, fi, tile - fi * p.tiles_per_field, s.tile);
   }
@@ -1700,21 +1732,20 @@ int validate_tables(const Job& j) {
 
 int64_t workspace_bytes(int64_t batch, int32_t num_fields);
 
-// The variant whose rows are 256 bytes (16 lanes of one 16-byte vector): the streamed tiles' shape
-// for fp32 / bf16 / fp16 tables.
+// The variant whose rows are 16 lane vectors (256 bytes of fp32 / bf16 / fp16, 128 bytes of int8):
+// the streamed tiles' shape.
 constexpr int kVarStream = 4;
 static_assert(StreamShape<float, 1 << kVarStream, 1>::ok && StreamShape<bf16_t, 1 << kVarStream, 1>::ok &&
-                  StreamShape<f16_t, 1 << kVarStream, 1>::ok && !StreamShape<i8_t, 1 << kVarStream, 1>::ok &&
+                  StreamShape<f16_t, 1 << kVarStream, 1>::ok && StreamShape<i8_t, 1 << kVarStream, 1>::ok &&
                   TileShape<bf16_t, 1 << kVarStream, 1>::NB == kRounds * (kWave / 16),
               "the streamed shape is variant kVarStream");
 
 // Whether a job's fields of the streamed shape may take streamed tiles (launch_shape also needs
-// buffer loads over every table of their launch): no binning, the default short-bag limit,
-// unquantised tables, and walks / id offsets that fit 32 bits.
+// buffer loads over every table of their launch): no binning, the default short-bag limit, and
+// walks / id offsets that fit 32 bits.
 bool stream_variant_allowed(const Job& j) {
   const int64_t nb = kRounds * (kWave / 16);  // bags per tile of the streamed shape
-  return !j.use_bins && j.sub_threshold == 0 && j.tdt != CTI_EBAG_I8 && j.nnz < INT32_MAX / nb &&
-         j.nnz * (j.idx32 ? 4 : 8) < (int64_t{1} << 32);
+  return !j.use_bins && j.sub_threshold == 0 && j.nnz < INT32_MAX / nb && j.nnz * (j.idx32 ? 4 : 8) < (int64_t{1} << 32);
 }
 
 int run_job(const Job& j, hipStream_t stream) {
@@ -1737,7 +1768,7 @@ int run_job(const Job& j, hipStream_t stream) {
   // whose rows are one lane vector per lane but of different widths form one mixed group.
   std::vector<int> var(j.num_fields);
   for (int f = 0; f < j.num_fields; ++f) var[f] = pick_variant(j.tables[f], tb, ob, j.out, j.out_row_stride);
-  // Fields of 256-byte rows that may take streamed tiles keep a launch of their own, so a field is
+  // Fields of the streamed shape that may take streamed tiles keep a launch of their own, so a field is
   // pooled the same way whatever other fields share the call.
   const bool stream_apart = stream_variant_allowed(j);
   int one_vec_shapes = 0;

@@ -439,8 +439,8 @@ def embedding_bag_pooled(
                [B, sum(D_f)] of that dtype.
       long_threshold  bags longer than this are split over the lane groups of a wavefront
                (0 = per-shape default, -1 = split every non-empty bag). At the default,
-               256-byte rows (fp32 D=64, bf16/fp16 D=128) without binning are streamed: every
-               bag is a sequential fp32 sum, whatever its length.
+               256-byte rows (fp32 D=64, bf16/fp16 D=128) and int8 D=128 rows without binning
+               are streamed: every bag is a sequential fp32 sum, whatever its length.
       use_bins  run the device length-binning pass: bags longer than ``block_threshold``
                (0 = default 512) are pooled by a second kernel: one wavefront per bag up to
                ``split_threshold`` rows (0 = default 192), longer bags split across the

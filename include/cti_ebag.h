@@ -84,7 +84,8 @@ typedef struct cti_ebag_table {
  *                    lane groups of a wavefront (partials combined in a fixed order).
  *                    0 = default; a negative value splits every non-empty bag (used by tests).
  *                    At the default, fields of 256-byte rows (fp32 D = 64, bf16 / fp16 D = 128)
- *                    without binning take streamed tiles instead: one wavefront walks a tile's
+ *                    and int8 D = 128 rows without binning take streamed tiles instead: one
+ *                    wavefront walks a tile's
  *                    rows in order, so every bag, whatever its length, is a sequential fp32 sum.
  *   use_bins:        1 = run the device length-binning pass first: bags longer than
  *                    block_threshold are listed in the workspace and pooled by a second kernel

@@ -183,3 +183,49 @@ def test_walks_ending_at_step_and_chunk_edges(pkg, dev):
         want32 = orc.pool_c(narrow, offsets, [table], "bf16", pooling, "f32")
         got32 = pooled(pkg, dev, narrow, offsets, [table], "bf16", pooling, "f32", idx=torch.int32)
         assert np.array_equal(got32, want32), pooling
+
+
+# int8 tables of 128-byte rows (D = 128): 2 bytes of every row per lane and the row's scale read
+# with it; each element accumulates fma(q, scale, acc) in row order, as the oracle's int8 loop.
+def _int8_case(seed, F, B, V, long_every=0, long_len=0, max_len=60):
+    rng = np.random.default_rng(seed)
+    L = rng.integers(0, max_len + 1, size=(F, B))
+    L[rng.random((F, B)) < 0.1] = 0
+    if long_every:
+        L[:, ::long_every] = long_len
+    ids = np.concatenate([make_ids(rng, int(L[f].sum()), V) for f in range(F)])
+    offsets = np.concatenate([[0], np.cumsum(L.reshape(-1))]).astype(np.int64)
+    tables = [(rng.integers(-128, 128, (V, 128)).astype(np.int8),
+               (rng.random(V) * 0.02 + 1e-4).astype(np.float32)) for _ in range(F)]
+    return ids, offsets, tables
+
+
+def _int8_pooled(pkg, dev, values, offsets, tables, pooling, odt, idx=torch.int64):
+    v = torch.from_numpy(np.ascontiguousarray(values)).to(dev, idx)
+    o = torch.from_numpy(np.ascontiguousarray(offsets)).to(dev)
+    t = [(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)) for q, s in tables]
+    out = pkg.embedding_bag_pooled(v, o, t, pooling=pooling, out_dtype=TORCH_DT[odt])
+    torch.cuda.synchronize()
+    return to_np(out, odt)
+
+
+@pytest.mark.parametrize("odt", ["bf16", "f32", "f16"])
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+@pytest.mark.parametrize("idx", [torch.int64, torch.int32])
+def test_int8_every_length_bitwise(pkg, dev, odt, pooling, idx):
+    """Lengths 0..60 with every fifth bag 300 rows; fp32 / fp16 outputs take the reference's bf16
+    rounding of each result first."""
+    print(f"stream int8 out={odt} {pooling} {idx}", flush=True)
+    ids, offsets, tables = _int8_case(len(odt) + len(pooling), F=4, B=37, V=900, long_every=5, long_len=300)
+    values = ids if idx == torch.int64 else np.clip(ids, -2 ** 31, 2 ** 31 - 1).astype(np.int32)
+    want = orc.pool_c(values, offsets, tables, "i8", pooling, odt)
+    assert np.array_equal(_int8_pooled(pkg, dev, values, offsets, tables, pooling, odt, idx=idx), want)
+
+
+def test_int8_malformed_offsets_match_oracle(pkg, dev):
+    rng = np.random.default_rng(17)
+    ids, offsets, tables = _int8_case(18, F=4, B=45, V=700, max_len=20)
+    bad = _malformed(offsets, ids.size, rng)
+    for pooling in ("sum", "mean"):
+        want = orc.pool_c(ids, bad, tables, "i8", pooling, "bf16")
+        assert np.array_equal(_int8_pooled(pkg, dev, ids, bad, tables, pooling, "bf16"), want), pooling
