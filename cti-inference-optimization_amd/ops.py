@@ -510,7 +510,9 @@ class PooledEmbedding:
     offsets passes the next batch's device offsets with each call
     (``plan(values, offsets, out, next_offsets=...)``): the launch also sorts that batch's tiles,
     most rows per bag first within each XCD's share, and the next call follows that order, which
-    shortens the drain at the end of its launch. The plan alternates two device order buffers;
+    shortens the drain at the end of its launch (on tables of 256-byte rows the order's own
+    workgroups now cost about as much as the order saves: measure it). The plan alternates two
+    device order buffers;
     the output is the same bit for bit with or without an order, whatever batch comes next. Only
     for jobs of one tiled row shape without binning (the library raises otherwise).
     """
