@@ -511,8 +511,8 @@ class PooledEmbedding:
     (``plan(values, offsets, out, next_offsets=...)``): the launch also sorts that batch's tiles,
     most rows per bag first within each XCD's share, and the next call follows that order, which
     shortens the drain at the end of its launch (on tables of 256-byte rows the order's own
-    workgroups now cost about as much as the order saves: measure it). The plan alternates two
-    device order buffers;
+    workgroups cost more than the order saves: 4,096 x 28 bags, 33.5 against 31.8 us without an
+    order). The plan alternates two device order buffers;
     the output is the same bit for bit with or without an order, whatever batch comes next. Only
     for jobs of one tiled row shape without binning (the library raises otherwise).
     """
