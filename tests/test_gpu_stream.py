@@ -1,6 +1,6 @@
-"""Streamed tiles on the GPU: 256-byte rows (bf16 / fp16 D = 128, fp32 D = 64) without binning and
-with the default short-bag limit, where a wavefront walks a tile's rows in order across bag
-boundaries.
+"""Streamed tiles on the GPU: 256-byte rows (bf16 / fp16 D = 128, fp32 D = 64) and 128-byte int8 rows
+(D = 128, each row's scale read beside it) without binning and with the default short-bag limit,
+where a wavefront walks a tile's rows in order across bag boundaries.
 
 Bar: every bag, whatever its length, equals the oracle's sequential fp32 sum bit for bit (sum and
 mean, every output type, int32 and int64 ids, with and without a dispatch order); malformed
