@@ -621,6 +621,15 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, Rsrc
   const bool contiguous = __ballot(valid && lane < nb - 1 && end != next_start) == 0;
   const int64_t s0 = shfl_i64(start, 0);
   const int len = valid ? static_cast<int>(end - start) : 0;
+  // mean pooling: lane i holds bag i's 1 / L (fp64, correctly rounded) and L (fp32), computed for
+  // all the tile's bags at once; a bag's flush reads its pair with readlane (L there is this len)
+  const bool mean = p.pooling == CTI_EBAG_MEAN;
+  double inv_lane = 0.0;
+  float len_f = 1.f;
+  if (mean && len > 0) {
+    inv_lane = 1.0 / static_cast<double>(len);
+    len_f = static_cast<float>(len);
+  }
   int cend = static_cast<int>(end - s0);
   if (!contiguous) {
     cend = len;
@@ -692,7 +701,13 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, Rsrc
       float r[E];
 #pragma unroll
       for (int i = 0; i < E; ++i) r[i] = acc[i];
-      if (p.pooling == CTI_EBAG_MEAN && L > 0) div_by_count<E>(r, 1.0 / static_cast<double>(L), static_cast<float>(L));
+      if (mean && L > 0) {
+        const uint64_t iv = __builtin_bit_cast(uint64_t, inv_lane);
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(iv), bag));
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(iv >> 32), bag));
+        const float fl = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, len_f), bag));
+        div_by_count<E>(r, __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo), fl);
+      }
       round_like_reference<TT, E>(p, r);
       store(bag, r);
 #pragma unroll
