@@ -33,10 +33,14 @@ the workload's batches are pooled once, and each step normalises one pooled bloc
 [B, sum(D)] (rows/s; roofline bytes = the block read and written plus gamma and beta).
 
 Printed (one JSON line): pooled bags/s over the timed steps, plus
-  roofline     algorithmic bytes per launch / mean launch duration (one pair of HIP events
-               around the K timed launches, on the stream the kernels run on), against 8 TB/s;
-               `traffic` is the HBM traffic per launch from the rocprofv3 FETCH_SIZE /
-               WRITE_SIZE summary committed under profiles/ (null when absent)
+  roofline     HBM bytes per launch / mean launch duration (one pair of HIP events around the
+               K timed launches, on the stream the kernels run on), against 8 TB/s: `traffic` is
+               the HBM traffic per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+               committed under profiles/ (`achieved` and `frac` are null when it is absent);
+               `effective_gbs` / `effective_frac` count every lookup's row (the algorithmic
+               bytes, which L2 / MALL hits let pass the peak), `compulsory_*` each distinct row
+               once
+  plain_launch the same steps without a dispatch order (when the batches carry one)
   cpu_baseline the reference's CPU pooling loop (F.embedding_bag per field, the oracle's
                restatement) on this host, on a bounded sample of the same batch
 """
@@ -92,15 +96,28 @@ def traffic_from_profiles(workload, kernel="pool_kernel", keys=("hbm_bytes_per_l
     return None, None
 
 
-def roofline(achieved_gbs, nbytes, launch_s, kernel, traffic_key=None, **extra):
-    """The bench line's roofline object. `achieved` is algorithmic bytes / mean launch time;
-    `dram_frac` is the HBM traffic the counters measured for one launch of the same kernel and
-    workload (`traffic`, from `traffic_source`) moved in the mean launch time, against the peak."""
+def roofline(nbytes, launch_s, kernel, traffic_key=None, compulsory_bytes=None, streaming=False, **extra):
+    """The bench line's roofline object for one kernel launch of `launch_s` seconds (mean).
+
+    `achieved` / `frac` are HBM bytes moved per second against the 8 TB/s peak: the HBM traffic
+    the rocprofv3 FETCH_SIZE / WRITE_SIZE passes measured for one launch of the same kernel and
+    workload (`traffic`, read from `traffic_source`), or, for a streaming kernel that reads and
+    writes each of its bytes once (`streaming`), its algorithmic bytes. Without either, `achieved`
+    is null. `effective_gbs` / `effective_frac` count every lookup's row (the algorithmic bytes
+    `nbytes`, most of them served by L2 / MALL under Zipf ids, so they can pass the peak), and
+    `compulsory_gbs` / `compulsory_frac` each distinct row once."""
     traffic, source = traffic_from_profiles(*traffic_key) if traffic_key else (None, None)
-    rec = {"bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-           "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic,
-           "dram_frac": traffic / launch_s / 1e9 / HBM_PEAK_GBS if traffic else None,
-           "traffic_source": source, "kernel": kernel, "bytes_per_launch": nbytes, "launch_us_mean": launch_s * 1e6}
+    if traffic is None and streaming:
+        traffic, source = nbytes, "algorithmic bytes (each byte read or written once)"
+    achieved = traffic / launch_s / 1e9 if traffic else None
+    rec = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": achieved / HBM_PEAK_GBS if achieved else None, "traffic": traffic,
+           "traffic_source": source, "kernel": kernel, "launch_us_mean": launch_s * 1e6,
+           "bytes_per_launch": nbytes, "effective_gbs": nbytes / launch_s / 1e9,
+           "effective_frac": nbytes / launch_s / 1e9 / HBM_PEAK_GBS}
+    if compulsory_bytes is not None:
+        rec.update(compulsory_bytes_per_launch=compulsory_bytes, compulsory_gbs=compulsory_bytes / launch_s / 1e9,
+                   compulsory_frac=compulsory_bytes / launch_s / 1e9 / HBM_PEAK_GBS)
     rec.update(extra)
     return rec
 
@@ -392,8 +409,7 @@ def bench_encoder(args, pkg, wls, dev):
                                "table, sum pooling, then LayerNorm over [B, 28*128]"},
         "us_per_step": {"pool_then_layernorm": t_sep * 1e6, "fused": t_fused * 1e6,
                         "pool_drop_in": t_plain * 1e6, "pool_drop_in_host_order": t_ordered * 1e6},
-        "roofline": roofline(achieved, fused_bytes, t_fused, "pool_norm_kernel",
-                             (args.workload + "-shared", "pool_norm_kernel")),
+        "roofline": roofline(fused_bytes, t_fused, "pool_norm_kernel", (args.workload + "-shared", "pool_norm_kernel")),
         "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
@@ -510,17 +526,16 @@ def bench_reference(args, pkg, dev):
         "config": {"workload": f"reference-5m: {WORKLOAD_TEXT['reference-5m']}",
                    "nnz_mean": float(np.mean([wl.nnz for wl in wls]))},
         "us_per_step": us,
-        "roofline": roofline(pool_bytes / t / 1e9, pool_bytes, t, "pool_kernel", ("reference-5m", "pool_kernel")),
+        "roofline": roofline(pool_bytes, t, "pool_kernel", ("reference-5m", "pool_kernel")),
         "cpu_baseline": None,
     }
     if "fused" in legs:
         tf = us["pool_layernorm_fused"] / 1e6
-        rec["roofline_fused_layernorm"] = roofline(fused_bytes / tf / 1e9, fused_bytes, tf, "pool_norm_kernel",
+        rec["roofline_fused_layernorm"] = roofline(fused_bytes, tf, "pool_norm_kernel",
                                                    ("reference-5m", "pool_norm_kernel"))
     if "int8" in legs:
         ti = us["pool_int8"] / 1e6
-        rec["roofline_int8"] = roofline(int8_bytes / ti / 1e9, int8_bytes, ti, "pool_kernel",
-                                        ("reference-5m-int8", "pool_kernel"))
+        rec["roofline_int8"] = roofline(int8_bytes, ti, "pool_kernel", ("reference-5m-int8", "pool_kernel"))
     if wl4:
         b4_bytes = float(np.mean([alg_bytes(wl) for wl in wl4]))
         rec["addressing"] = {
@@ -666,7 +681,7 @@ def bench_layout(args, pkg, dev):
                         "reference_pack": wall_ref_pack * 1e6, "reference_pack_gpu": k_ref_pack * 1e6,
                         "device_pack_python": wall_pack * 1e6, "device_pack_raw": wall_pack_raw * 1e6,
                         "device_pack_gpu": k_pack * 1e6},
-        "roofline": roofline(achieved, merge_bytes, k_merge, "merge_kernel", None,
+        "roofline": roofline(merge_bytes, k_merge, "merge_kernel", streaming=True,
                              pack_bytes_per_launch=pack_bytes, pack_achieved=pack_bytes / k_pack / 1e9),
         "cpu_baseline": {"value": lazy.batch * F / t_ref_merge, "unit": "bags/s", "cores": torch.get_num_threads(),
                          "kind": "port", "sample": "the reference merge (torch ops on host tensors) of the same "
@@ -711,10 +726,25 @@ def bench_layernorm(args, pkg, plan, inputs, wl0, dev):
         "data": "synthetic: pooled blocks of 4 seeded index sets rotated",
         "config": {"workload": f"layernorm over the pooled {args.workload} block", "rows": blocks[0].shape[0],
                    "cols": width},
-        "roofline": roofline(achieved, nbytes, launch_s, "norm_rows_kernel", None),
+        "roofline": roofline(nbytes, launch_s, "norm_rows_kernel", streaming=True),
         "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)
+
+
+def main_kernel_name(wl, args):
+    """The pooling launch sequence's kernels: fields of several row widths share one mixed-width
+    launch sequence; binning adds its pass and the list kernel."""
+    main_kernel = "pool_mixed_kernel" if len(set(wl.dims)) > 1 else "pool_kernel"
+    return f"bin_kernel + {main_kernel} + pool_long_kernel" if args.bins else main_kernel
+
+
+def main_prof_kernel(wl, args):
+    """The name under which the launch sequence's profiles are kept in profiles/."""
+    mixed = len(set(wl.dims)) > 1
+    if args.bins:
+        return "bin_mixed_long_kernels" if mixed else "bin_pool_long_kernels"
+    return "pool_mixed_kernel" if mixed else "pool_kernel"
 
 
 def main():
@@ -833,18 +863,21 @@ def main():
     # Timed region: K back-to-back steps, bracketed by one pair of HIP events recorded on the
     # stream the kernels run on (per-step events would add a gap between kernels).
     K = args.steps
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
+
+    def timed_region(step_fn):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        for i in range(args.warmup, args.warmup + K):  # continues the warm-up's sequence of index sets
+            step_fn(i)
+        ev1.record()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, ev0.elapsed_time(ev1) / 1e3 / K
+
     log(f"timing {K} steps")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record()
-    for i in range(args.warmup, args.warmup + K):  # continues the warm-up's sequence of index sets
-        step(i)
-    ev1.record()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    mean_launch_s = ev0.elapsed_time(ev1) / 1e3 / K
+    elapsed, mean_launch_s = timed_region(step)
     timed = range(args.warmup, args.warmup + K)
     used_bytes = float(np.mean([bytes_alg[i % args.sets] for i in timed]))
     used_comp = float(np.mean([bytes_comp[i % args.sets] for i in timed]))
@@ -853,6 +886,22 @@ def main():
     achieved = used_bytes / mean_launch_s / 1e9
     log(f"{ms_per_step * 1e3:.1f} us/step wall, {mean_launch_s * 1e6:.1f} us/step on the GPU, "
         f"{achieved:.0f} GB/s algorithmic, {used_comp / mean_launch_s / 1e9:.0f} GB/s compulsory")
+
+    plain = None
+    if orders is not None or args.dispatch_order == "launch":
+        # the same steps without a dispatch order: what the reference's call site gets with no
+        # change to the batch's producer
+        for i in range(200):
+            plan(*inputs[i % args.sets], out)
+        plain_elapsed, plain_launch_s = timed_region(lambda i: plan(*inputs[i % args.sets], out))
+        log(f"without a dispatch order: {plain_launch_s * 1e6:.1f} us/step on the GPU")
+        plain = {"dispatch_order": "off", "value": wl0.num_bags / (plain_elapsed / K), "unit": "bags/s",
+                 "ms_per_step": plain_elapsed / K * 1e3,
+                 "roofline": roofline(used_bytes, plain_launch_s, main_kernel_name(wl0, args),
+                                      None if args.index_dtype == "int32" else
+                                      (args.workload + ("-int8" if args.int8 else ""), main_prof_kernel(wl0, args),
+                                       ("hbm_bytes_per_launch_order_off", "hbm_bytes_per_launch")),
+                                      compulsory_bytes=used_comp)}
 
     accuracy = None
     if args.int8:
@@ -873,11 +922,8 @@ def main():
         if args.int8:
             cpu["sample"] += " (the reference's CPU path has no int8 tables: this is its float loop)"
 
-    # fields of several row widths share one mixed-width launch sequence
-    mixed = len(set(wl0.dims)) > 1
-    main_kernel = "pool_mixed_kernel" if mixed else "pool_kernel"
-    kernel_name = f"bin_kernel + {main_kernel} + pool_long_kernel" if args.bins else main_kernel
-    prof_kernel = ("bin_mixed_long_kernels" if mixed else "bin_pool_long_kernels") if args.bins else main_kernel
+    kernel_name = main_kernel_name(wl0, args)
+    prof_kernel = main_prof_kernel(wl0, args)
     rec = {
         "metric": METRIC,
         "value": value,
@@ -901,13 +947,14 @@ def main():
                    "length_binning": bool(args.bins), "int8_tables": bool(args.int8),
                    "dispatch_order": args.dispatch_order, "index_dtype": args.index_dtype},
         # the profiles' counters were taken with int64 ids: int32 launches report no traffic
-        "roofline": roofline(achieved, used_bytes, mean_launch_s, kernel_name,
+        "roofline": roofline(used_bytes, mean_launch_s, kernel_name,
                              None if args.index_dtype == "int32" else
                              (args.workload + ("-int8" if args.int8 else ""), prof_kernel,
                               {"host": ("hbm_bytes_per_launch",),
                                "launch": ("hbm_bytes_per_launch_order_launch", "hbm_bytes_per_launch"),
                                "off": ("hbm_bytes_per_launch_order_off", "hbm_bytes_per_launch")}[args.dispatch_order]),
-                             compulsory_bytes_per_launch=used_comp),
+                             compulsory_bytes=used_comp),
+        "plain_launch": plain,
         "cpu_baseline": cpu,
     }
     if accuracy is not None:

@@ -197,8 +197,10 @@ def move_model_inputs_to_device(batch: dict, device, slot_num: int = 28,
     non_blocking=True)`` as in the reference (val_offsets widened to int64, :747). Batches that
     carry only the per-slot pairs ``{i+1: (values, offsets)}`` are moved slot by slot and packed
     on the device by one kernel (``pack_slots``) instead of two ``torch.cat`` and a host tensor
-    (:750-762). Every other string key of the batch (the later stages' inputs, which this path
-    does not read) is passed through with its tensors moved to the device.
+    (:750-762). The attention stage's inputs are passed on as the reference passes them
+    (:763-778): ``_attn_groups`` with every tensor inside it moved to the device, and
+    ``user_offsets`` only when the batch has no ``_attn_groups`` (the model takes the
+    varlen-attention path when it finds ``user_offsets``). No other key is moved.
     """
     device = torch.device(device)
     if "_flat_values" in batch:
@@ -216,7 +218,8 @@ def move_model_inputs_to_device(batch: dict, device, slot_num: int = 28,
             vals, offs = batch[s]
             slots.append((vals.to(device, non_blocking=True).long(), offs.to(device, non_blocking=True).long()))
         model_batch = dict(pack_slots(slots))
-    for key, value in batch.items():
-        if isinstance(key, str) and key not in model_batch and key not in _PARTS:
-            model_batch[key] = _to_device(value, device)
+    if "_attn_groups" in batch:
+        model_batch["_attn_groups"] = _to_device(batch["_attn_groups"], device)
+    elif "user_offsets" in batch:
+        model_batch["user_offsets"] = batch["user_offsets"].to(device, non_blocking=True)
     return model_batch

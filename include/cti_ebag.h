@@ -84,9 +84,12 @@ typedef struct cti_ebag_table {
  *                    lane groups of a wavefront (partials combined in a fixed order).
  *                    0 = default; a negative value splits every non-empty bag (used by tests).
  *                    At the default, fields of 256-byte rows (fp32 D = 64, bf16 / fp16 D = 128)
- *                    and int8 D = 128 rows without binning take streamed tiles instead: one
- *                    wavefront walks a tile's
- *                    rows in order, so every bag, whatever its length, is a sequential fp32 sum.
+ *                    and int8 D = 128 rows take streamed tiles instead: one wavefront walks a
+ *                    tile's rows in order, so every bag, whatever its length, is a sequential
+ *                    fp32 sum. Conditions: no binning, nnz < 2^28 and nnz * sizeof(id) < 4 GiB,
+ *                    and every table of the streamed group with a power-of-two row stride in
+ *                    bytes and (rows + 1) * row stride <= 4 GiB. Otherwise those fields take the
+ *                    length-ranked tiles and bags above 24 rows are split as described above.
  *   use_bins:        1 = run the device length-binning pass first: bags longer than
  *                    block_threshold are listed in the workspace and pooled by a second kernel
  *                    (one wavefront per bag, or, above split_threshold, the wavefronts of a

@@ -13,8 +13,15 @@ FORBIDDEN = re.compile(r"^\s+s_(store|atomic|buffer_store|buffer_atomic|dcache_w
                        re.M)
 
 
-@pytest.mark.parametrize("src", ["ebag_pool.hip", "ebag_layout.hip", "ebag_status.hip", "ebag_norm.hip",
-                                 "ebag_quant.hip"])
+SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def test_every_hip_source_is_guarded():
+    assert {"ebag_pool.hip", "ebag_layout.hip", "ebag_status.hip", "ebag_norm.hip", "ebag_quant.hip",
+            "ebag_static.hip"} <= set(SOURCES)
+
+
+@pytest.mark.parametrize("src", SOURCES)
 def test_no_scalar_cache_writes(src, tmp_path):
     out = tmp_path / (src + ".s")
     cmd = ["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",

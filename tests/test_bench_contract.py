@@ -39,12 +39,20 @@ def test_missing_profile_gives_null_traffic(bench):
     assert bench.traffic_from_profiles("no-such-workload") == (None, None)
 
 
-def test_roofline_reports_the_dram_fraction(bench):
-    r = bench.roofline(6000.0, 240e6, 40e-6, "pool_kernel", ("bf16-2m", "pool_kernel"))
-    assert r["frac"] == pytest.approx(0.75)
-    assert r["dram_frac"] == pytest.approx(r["traffic"] / 40e-6 / 1e9 / 8000.0)
+def test_roofline_frac_is_the_measured_hbm_fraction(bench):
+    # achieved / frac: the profile's HBM bytes per launch over the launch time, against 8 TB/s;
+    # the algorithmic bytes (every lookup's row) go to effective_*
+    r = bench.roofline(240e6, 40e-6, "pool_kernel", ("bf16-2m", "pool_kernel"), compulsory_bytes=100e6)
     assert r["traffic_source"] == "profiles/pool_kernel_bf16-2m.md"
-    assert bench.roofline(1.0, 1.0, 1.0, "k", None)["dram_frac"] is None
+    assert r["achieved"] == pytest.approx(r["traffic"] / 40e-6 / 1e9)
+    assert r["frac"] == pytest.approx(r["achieved"] / 8000.0)
+    assert r["effective_gbs"] == pytest.approx(6000.0) and r["effective_frac"] == pytest.approx(0.75)
+    assert r["compulsory_frac"] == pytest.approx(100e6 / 40e-6 / 1e9 / 8000.0)
+    # no counter profile: no HBM figure, unless the kernel streams each byte once
+    none = bench.roofline(1.0, 1.0, "k", None)
+    assert none["achieved"] is None and none["frac"] is None and none["traffic"] is None
+    streamed = bench.roofline(8e6, 1e-6, "k", None, streaming=True)
+    assert streamed["frac"] == pytest.approx(1.0) and streamed["traffic"] == 8e6
 
 
 def test_host_cpu_counts(bench):

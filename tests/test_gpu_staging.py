@@ -137,21 +137,34 @@ def test_per_slot_pairs_are_packed_on_device(pkg, dev, weight):
         assert torch.equal(moved[k].cpu(), hb[k])
 
 
-def test_other_batch_keys_pass_through(pkg, dev):
-    """Keys the pooling step does not read are passed on, their tensors moved to the device
-    (nested lists / dicts too) and everything else unchanged."""
+def test_attention_keys_pass_through_as_the_reference_moves_them(pkg, dev):
+    """online_best/infer.py:762-778: ``_attn_groups`` is moved (its tensors to the device, the
+    rest unchanged); ``user_offsets`` is moved only when there are no ``_attn_groups``; the
+    batch's other keys (label, logid, pred_mask, ...) are not part of the model batch."""
     rng = np.random.default_rng(12)
     hb, B = host_batch(rng, 9, wide_ids=False)
     hb = dict(hb)
     hb["user_offsets"] = torch.arange(4)
-    hb["_attn_groups"] = [{"rows": torch.arange(3), "num_users": 2, "identity": True}]
-    for stager in (None, pkg.InputStager(hb["_flat_values"].numel(), S, B, dev)):
-        moved = pkg.move_model_inputs_to_device(hb, dev, S, stager=stager)
-        assert moved["user_offsets"].device.type == "cuda" and torch.equal(moved["user_offsets"].cpu(), torch.arange(4))
-        grp = moved["_attn_groups"][0]
-        assert grp["rows"].device.type == "cuda" and grp["num_users"] == 2 and grp["identity"] is True
-        got = pool(pkg, moved, weight_of(dev), B)
-        torch.cuda.synchronize()
-        assert np.array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16), oracle_pool(hb, weight_of(dev), B))
-        if stager is not None:
-            stager.release(moved)
+    hb["label"] = torch.zeros(B)
+    hb["logid"] = ["a"] * B
+    for with_groups in (True, False):
+        batch = dict(hb)
+        if with_groups:
+            batch["_attn_groups"] = [{"rows": torch.arange(3), "num_users": 2, "identity": True}]
+        for stager in (None, pkg.InputStager(hb["_flat_values"].numel(), S, B, dev)):
+            moved = pkg.move_model_inputs_to_device(batch, dev, S, stager=stager)
+            assert "label" not in moved and "logid" not in moved
+            if with_groups:
+                assert "user_offsets" not in moved
+                grp = moved["_attn_groups"][0]
+                assert grp["rows"].device.type == "cuda" and grp["num_users"] == 2 and grp["identity"] is True
+            else:
+                assert "_attn_groups" not in moved
+                assert moved["user_offsets"].device.type == "cuda"
+                assert torch.equal(moved["user_offsets"].cpu(), torch.arange(4))
+            got = pool(pkg, moved, weight_of(dev), B)
+            torch.cuda.synchronize()
+            assert np.array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16),
+                                  oracle_pool(hb, weight_of(dev), B))
+            if stager is not None:
+                stager.release(moved)

@@ -229,3 +229,39 @@ def test_int8_malformed_offsets_match_oracle(pkg, dev):
     for pooling in ("sum", "mean"):
         want = orc.pool_c(ids, bad, tables, "i8", pooling, "bf16")
         assert np.array_equal(_int8_pooled(pkg, dev, ids, bad, tables, pooling, "bf16"), want), pooling
+
+
+@pytest.mark.parametrize("tdt,D,stride", [("bf16", 128, 136), ("f32", 64, 72)])
+def test_padded_table_takes_the_ranked_tiles(pkg, dev, tdt, D, stride):
+    """A table whose row stride in bytes is not a power of two cannot be read by buffer loads, so
+    its 256-byte rows take the length-ranked tiles: bags of up to 24 rows are still sequential
+    sums (bit for bit), longer bags are split and meet the fp32 reassociation bound; the padding
+    columns are never read (they hold NaN)."""
+    case = random_case(D + stride, F=4, B=45, dims=(D,), V=(700,), max_len=60, tdt=tdt, long_every=3,
+                       long_len=200)
+    B = 45
+    padded = []
+    for t in case.tables:
+        p = np.zeros((t.shape[0], stride), dtype=t.dtype)
+        p[:, :D] = t
+        p[:, D:] = np.float32("nan") if tdt == "f32" else 0x7FC0
+        padded.append(to_dev(p, tdt, dev)[:, :D])
+    v = torch.from_numpy(case.values).to(dev)
+    o = torch.from_numpy(case.offsets).to(dev)
+    out = pkg.embedding_bag_pooled(v, o, padded, pooling="sum", out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    want = orc.pool_c(case.values, case.offsets, case.tables, tdt, "sum", "f32")
+    lens = np.diff(case.offsets).reshape(4, B).T  # [B, F]
+    assert (lens > 24).sum() > 10
+    for f in range(4):
+        cols = slice(f * D, (f + 1) * D)
+        short = lens[:, f] <= 24
+        assert np.array_equal(got[short, cols], want[short, cols].astype(np.float64))
+        w = orc.decode(case.tables[f], tdt).astype(np.float64)
+        for b in np.nonzero(~short)[0]:
+            s, e = case.offsets[f * B + b], case.offsets[f * B + b + 1]
+            rows = w[np.clip(case.values[s:e], 0, w.shape[0] - 1)]
+            ref = rows.sum(axis=0)
+            bound = np.abs(rows).sum(axis=0) * (e - s) * 2.0 ** -24
+            assert np.all(np.abs(got[b, cols] - ref) <= bound * (1 + 2.0 ** -24) + np.abs(ref) * 2.0 ** -24 + 1e-30)

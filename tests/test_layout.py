@@ -101,6 +101,27 @@ def test_pair_merge_int32_round_trip():
     assert not np.array_equal(c[0], orc.merge_layouts(big, S)[0])  # ids >= 2^31 wrap there only
 
 
+def test_pair_merge_wraps_as_int32_does():
+    """The pair merge's .int() / .long() (online_best/infer.py:3008-3009, :3019-3020) is a
+    two's-complement wrap to int32: closed forms (2^31 + k -> k - 2^31, -2^31 - 5 -> 2^31 - 5,
+    2^32 + 7 -> 7) and torch's own .int().long() on the same ids. A saturating cast fails both."""
+    import torch
+
+    ids = np.array([2 ** 31 + 3, -2 ** 31 - 5, 2 ** 32 + 7, 2 ** 31 - 1, -2 ** 31, 5, -1, 2 ** 40 + 2 ** 31],
+                   dtype=np.int64)
+    want = np.array([3 - 2 ** 31, 2 ** 31 - 5, 7, 2 ** 31 - 1, -2 ** 31, 5, -1, -2 ** 31], dtype=np.int64)
+    S, B = 2, 2
+    lay = (ids, np.array([0, 3, 4, 0, 1, 4], np.int64), np.array([0, 4], np.int64))
+    empty = (np.zeros(0, np.int64), np.zeros(S * (B + 1), np.int64), np.zeros(S, np.int64))
+    v, o, vo = orc.merge_pair_layouts([lay, empty], S)
+    assert np.array_equal(v, want)
+    assert np.array_equal(v, torch.from_numpy(ids).int().long().numpy())
+    # offsets pass through the same casts; at these sizes they are unchanged
+    assert np.array_equal(o, orc.merge_layouts([lay, empty], S)[1]) and np.array_equal(vo, [0, 4])
+    # a saturating cast (the mistake this rejects) gives other ids
+    assert not np.array_equal(np.clip(ids, -2 ** 31, 2 ** 31 - 1), want)
+
+
 def test_workload_shapes(pkg):
     W = pkg.workloads
     wl = W.make("small-fp32", seed=0)

@@ -6,6 +6,7 @@ length-binning path (which is the one that uses the static workspace), a plain c
 mixed-width call; a binned job larger than the static workspace is refused before any launch.
 """
 import ctypes
+import types
 
 import numpy as np
 import pytest
@@ -46,6 +47,49 @@ def _call(pkg, dev, case, use_bins, static):
     c.check(rc)
     torch.cuda.synchronize()
     return out.cpu().numpy()
+
+
+def test_first_call_inside_graph_capture(pkg, dev):
+    """Defined first in the last-collected file, so that in a test run (and in a process of its
+    own) this is the first call of the entry on the device: it is made inside a HIP graph capture
+    (the setup on first use, a symbol lookup and a fill kernel for the list counters, is captured
+    with it), then the graph is replayed on two batches written into the captured buffers; each
+    replay equals cti_ebag_forward with a caller-allocated workspace, bit for bit."""
+    c = pkg._capi
+    lib = c.lib()
+    cases = [random_case(40 + k, F=7, B=120, dims=(128,), V=(900,), max_len=25, tdt="bf16", long_every=9,
+                         long_len=260 + 10 * k) for k in range(2)]
+    nnz = max(x.values.size for x in cases)
+    tt, descs, code, width = _tables(pkg, cases[0], dev)
+    v = torch.zeros(nnz, dtype=torch.int64, device=dev)
+    o = torch.zeros(cases[0].offsets.size, dtype=torch.int64, device=dev)
+    out = torch.zeros((cases[0].B, width), dtype=torch.float32, device=dev)
+    opts = c.Options()
+    opts.use_bins, opts.block_threshold, opts.split_threshold = 1, 32, 192
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.cti_ebag_forward_static(v.data_ptr(), c.I64, nnz, o.data_ptr(), cases[0].B, cases[0].F, descs, code,
+                                         c.SUM, out.data_ptr(), c.F32, width, ctypes.byref(opts), stream)
+    c.check(rc)
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for case in cases:
+            ids = np.zeros(nnz, np.int64)
+            ids[:case.values.size] = case.values
+            # bags past the case's nnz are never read: the offsets end at case.values.size
+            v.copy_(torch.from_numpy(ids))
+            o.copy_(torch.from_numpy(case.offsets))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = out.cpu().numpy().copy()
+            # the same batch over the captured tables (the first case's), eagerly
+            same_tables = types.SimpleNamespace(values=case.values, offsets=case.offsets, tables=cases[0].tables,
+                                                F=case.F, B=case.B)
+            want = _call(pkg, dev, same_tables, True, static=False)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (rep, case.values.size)
 
 
 CASES = [  # (seed, F, B, dims, max_len, long_every, long_len): the second call of each pair is smaller
