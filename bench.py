@@ -18,9 +18,10 @@ with int64 inputs, (c) the same with ids and offsets narrowed to int32 on the ho
 reports bags/s per variant, the copy-only and pool-only times, and the bytes moved per batch.
 
 `--stage encoder` times the encoder's front end on the workload's batches (reference layout, one
-shared table as in the reference, sum pooling): the pooling kernel followed by the LayerNorm
-kernel, against the fused kernel that normalises each pooled row on chip
-(online_best/infer.py:1050-1076).
+shared table as in the reference, sum pooling, online_best/infer.py:1050-1085): pooling, the
+LayerNorm statistics and the matrix-core kernel that normalises the pooled block's tiles as it
+loads them and multiplies them with the Linear(28*D -> 512) weight, against the pooling with the
+LayerNorm fused into it (or the two kernels) followed by torch's Linear; each kernel alone too.
 
 `--stage layout` times the device layout kernels against the reference's way of doing the same
 work: merging the 8 sub-batches of lazy-32k into one flat layout (online_best/infer.py:581-631,
@@ -380,6 +381,38 @@ def bench_encoder(args, pkg, wls, dev):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / args.steps / 1e3
 
+    # the encoder's Linear(F*D -> d_model) after the LayerNorm (online_best/infer.py:1085, nn.Linear
+    # of the reference's model, d_model = 512)
+    d_model = 512
+    lin_w = torch.empty((d_model, F * D), dtype=torch.bfloat16, device=dev).normal_(0.0, (F * D) ** -0.5, generator=g)
+    lin_b = torch.empty(d_model, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.1, generator=g)
+    y = torch.empty((B, d_model), dtype=torch.bfloat16, device=dev)
+    mean = torch.empty(B, dtype=torch.float32, device=dev)
+    rstd = torch.empty(B, dtype=torch.float32, device=dev)
+    gamma_b, beta_b = gamma.to(torch.bfloat16), beta.to(torch.bfloat16)
+
+    def front_mfma(i):  # RepEncoder.forward: pooling, statistics, LayerNorm inside the Linear
+        pool_ordered(i)
+        pkg.layer_norm_stats(out, 1e-5, mean, rstd)
+        pkg.layer_norm_linear(out, lin_w, lin_b, mean=mean, rstd=rstd, norm_weight=gamma_b, norm_bias=beta_b, out=y)
+
+    def front_fused_norm_torch_linear(i):  # pooling + LayerNorm in one kernel, then torch's Linear
+        fused(i)
+        torch.nn.functional.linear(out, lin_w, lin_b)
+
+    def front_separate_torch_linear(i):  # pooling, the LayerNorm kernel, torch's Linear
+        separate(i)
+        torch.nn.functional.linear(out, lin_w, lin_b)
+
+    def ln_linear_only(i):
+        pkg.layer_norm_linear(out, lin_w, lin_b, mean=mean, rstd=rstd, norm_weight=gamma_b, norm_bias=beta_b, out=y)
+
+    def torch_linear_only(i):
+        torch.nn.functional.linear(out, lin_w, lin_b)
+
+    def stats_only(i):
+        pkg.layer_norm_stats(out, 1e-5, mean, rstd)
+
     log("drop-in pooling, plain and with host-made orders")
     t_plain = timed(pool_plain)
     t_ordered = timed(pool_ordered)
@@ -387,29 +420,56 @@ def bench_encoder(args, pkg, wls, dev):
     t_sep = timed(separate)
     log("fused")
     t_fused = timed(fused)
+    log("front end with the Linear: statistics + LayerNorm-Linear kernel, and torch's Linear after the LayerNorm")
+    t_front = timed(front_mfma)
+    t_front_torch = timed(front_fused_norm_torch_linear)
+    t_front_sep = timed(front_separate_torch_linear)
+    pool_ordered(0)
+    pkg.layer_norm_stats(out, 1e-5, mean, rstd)
+    t_lin = timed(ln_linear_only)
+    t_tlin = timed(torch_linear_only)
+    t_stats = timed(stats_only)
     # the pooling's algorithmic bytes with the reference layout's offsets (row offsets + slot bases)
     pool_bytes = float(np.mean([wl.bytes_algorithmic() - wl.offsets.size * 8 + (F * (B + 1) + F) * 8 for wl in wls]))
     fused_bytes = pool_bytes + 2 * F * D * 2  # + gamma and beta
-    achieved = fused_bytes / t_fused / 1e9
+    lin_flops = 2.0 * B * d_model * F * D
+    lin_bytes = B * F * D * 2 + d_model * F * D * 2 + B * d_model * 2 + B * 8
+    log(f"front end {t_front * 1e6:.1f} us (pool+LN fused, torch Linear {t_front_torch * 1e6:.1f}; separate "
+        f"{t_front_sep * 1e6:.1f}); LayerNorm-Linear {t_lin * 1e6:.1f} us = {lin_flops / t_lin / 1e12:.0f} TFLOP/s, "
+        f"torch Linear {t_tlin * 1e6:.1f} us")
     rec = {
-        "metric": "pooled and normalised rows/sec (encoder front end), B=4096x28 fields, D=128 bf16",
-        "value": B / t_fused,
+        "metric": f"encoder front end rows/sec (pooling, input LayerNorm, Linear({F * D}->{d_model})), "
+                  f"B={B}x{F} fields, D={D} bf16",
+        "value": B / t_front,
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": t_fused * 1e3,
+        "ms_per_step": t_front * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": f"synthetic: {n} seeded index sets rotated, one shared N(0, 0.01) table [{V}, {D}], "
-                "gamma ~ N(1, 0.1), beta ~ N(0, 0.1)",
+                "gamma ~ N(1, 0.1), beta ~ N(0, 0.1), Linear weight ~ N(0, 1/K), bias ~ N(0, 0.1)",
         "config": {"workload": f"{args.workload}: {WORKLOAD_TEXT[args.workload]}; reference layout, one shared "
-                               "table, sum pooling, then LayerNorm over [B, 28*128]"},
-        "us_per_step": {"pool_then_layernorm": t_sep * 1e6, "fused": t_fused * 1e6,
+                               f"table, sum pooling, LayerNorm over [B, {F * D}], Linear to {d_model}"},
+        "us_per_step": {"front_end_pool_stats_layernorm_linear": t_front * 1e6,
+                        "front_end_pool_layernorm_fused_then_torch_linear": t_front_torch * 1e6,
+                        "front_end_pool_then_layernorm_then_torch_linear": t_front_sep * 1e6,
+                        "layernorm_linear_kernel": t_lin * 1e6, "torch_linear": t_tlin * 1e6,
+                        "layernorm_statistics": t_stats * 1e6,
+                        "pool_then_layernorm": t_sep * 1e6, "fused_pool_layernorm": t_fused * 1e6,
                         "pool_drop_in": t_plain * 1e6, "pool_drop_in_host_order": t_ordered * 1e6},
-        "roofline": roofline(fused_bytes, t_fused, "pool_norm_kernel", (args.workload + "-shared", "pool_norm_kernel")),
+        "roofline": {"bound": "mfma", "kernel": "ln_linear_kernel", "achieved": lin_flops / t_lin / 1e12,
+                     "peak": 2500.0, "unit": "TFLOP/s", "frac": lin_flops / t_lin / 1e12 / 2500.0,
+                     "flops_per_launch": lin_flops, "launch_us_mean": t_lin * 1e6,
+                     "hbm_bytes_per_launch_algorithmic": lin_bytes,
+                     "hbm_gbs_algorithmic": lin_bytes / t_lin / 1e9,
+                     "traffic": traffic_from_profiles(args.workload + "-shared", "ln_linear_kernel")[0],
+                     "torch_linear_tflops": lin_flops / t_tlin / 1e12},
+        "roofline_fused_pool_layernorm": roofline(fused_bytes, t_fused, "pool_norm_kernel",
+                                                  (args.workload + "-shared", "pool_norm_kernel")),
         "cpu_baseline": None,
     }
     print(json.dumps(rec), flush=True)

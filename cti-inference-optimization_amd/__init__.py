@@ -9,6 +9,8 @@ Public surface:
   embedding_bag_pooled       per-field tables, global offsets, sum/mean, chosen output dtype
   PooledEmbedding            the same with the table descriptors prepared once (serving loops)
   layer_norm                 the encoder's input LayerNorm over the pooled rows
+  layer_norm_stats           its per-row mean and rstd only
+  layer_norm_linear          the input LayerNorm and the encoder's Linear in one matrix-core kernel
   RepEncoder                 the reference module with the fused step and LayerNorm on this path
   collate_flat_layout, prebuild_flat_layout   host builders of the flat layout
   pack_slots, merge_batches                   GPU builders of the flat layout
@@ -22,8 +24,8 @@ from .encoder import RepEncoder
 from .layout import collate_flat_layout, merge_batches, pack_slots, prebuild_flat_layout
 from .staging import InputStager, move_model_inputs_to_device
 from .ops import (PooledEmbedding, embedding_bag_pooled, fused_all_slots_embedding, fused_all_slots_embedding_int8,
-                  fused_all_slots_embedding_layernorm, fused_embedding, layer_norm, make_tile_order, order_bytes,
-                  quantize_embedding_int8)
+                  fused_all_slots_embedding_layernorm, fused_embedding, layer_norm, layer_norm_linear,
+                  layer_norm_stats, make_tile_order, order_bytes, quantize_embedding_int8)
 
 __all__ = [
     "EbagError",
@@ -43,6 +45,8 @@ __all__ = [
     "fused_all_slots_embedding_layernorm",
     "quantize_embedding_int8",
     "layer_norm",
+    "layer_norm_stats",
+    "layer_norm_linear",
     "make_tile_order",
     "order_bytes",
     "workloads",

@@ -83,6 +83,7 @@ __global__ void __launch_bounds__(WAVES * kWave) norm_rows_kernel(const NormPara
     if (p.mean_out) p.mean_out[row] = mean;
     if (p.rstd_out) p.rstd_out[row] = rstd;
   }
+  if (!p.y) return;  // statistics only
   T* yr = reinterpret_cast<T*>(p.y + row * p.cols * Elem<T>::kBytes);
   with_stream(p.stream_out, [&](auto stream) {
 #pragma unroll
@@ -121,6 +122,7 @@ __global__ void __launch_bounds__(kNormThreads) norm_rows_loop_kernel(const Norm
     if (p.mean_out) p.mean_out[row] = mean;
     if (p.rstd_out) p.rstd_out[row] = rstd;
   }
+  if (!p.y) return;  // statistics only
   T* yr = reinterpret_cast<T*>(p.y + row * p.cols * Elem<T>::kBytes);
   with_stream(p.stream_out, [&](auto stream) {
     for (int64_t c = threadIdx.x; c < p.cols; c += kNormThreads) {
@@ -134,7 +136,7 @@ template <typename T, typename PT>
 hipError_t launch_norm(const NormParams& p, hipStream_t s) {
   constexpr int VEC = 16 / Elem<T>::kBytes;
   const auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
-  const bool aligned = a16(p.x) && a16(p.y) && a16(p.gamma) && a16(p.beta) && p.cols % VEC == 0;
+  const bool aligned = a16(p.x) && (!p.y || (a16(p.y) && a16(p.gamma) && a16(p.beta))) && p.cols % VEC == 0;
   const int64_t nvec = p.cols / VEC;
   const dim3 grid(static_cast<unsigned>(p.rows));
   const dim3 one(kWave), four(4 * kWave);
@@ -181,7 +183,10 @@ extern "C" int cti_ebag_layernorm(const void* x, void* y, int64_t rows, int64_t 
   if (!(eps >= 0.f)) return set_error(CTI_EBAG_EINVAL, "eps must be >= 0");
   if (rows == 0) return CTI_EBAG_OK;
   if (rows > INT32_MAX) return set_error(CTI_EBAG_EUNSUPPORTED, "more than 2^31 - 1 rows (%lld)", (long long)rows);
-  if (!x || !y || !gamma || !beta) return set_error(CTI_EBAG_EINVAL, "NULL device pointer among x/y/gamma/beta");
+  if (!x) return set_error(CTI_EBAG_EINVAL, "x is NULL");
+  if (!y && !(mean_out && rstd_out))
+    return set_error(CTI_EBAG_EINVAL, "y is NULL: a statistics-only call needs both mean_out and rstd_out");
+  if (y && (!gamma || !beta)) return set_error(CTI_EBAG_EINVAL, "NULL device pointer among gamma/beta");
   NormParams p;
   p.x = static_cast<const char*>(x);
   p.y = static_cast<char*>(y);

@@ -5,8 +5,9 @@ names, forward(batch) contract): the 28 slots are pooled into ``[B, slot_num*emb
 table's dtype and normalised with the ``input_norm`` parameters (the reference's Triton
 LayerNorm, online_best/infer.py:1061-1076) by one fused kernel
 (``fused_all_slots_embedding_layernorm``; ``pooled`` alone uses ``fused_all_slots_embedding``),
-and ``linear`` (torch's Linear, a plain library GEMM) maps them to d_model
-(online_best/infer.py:1084). Like the reference's Triton kernels, the pooling and the
+and ``linear`` maps them to d_model (online_best/infer.py:1085): for the bf16 model, one
+matrix-core kernel applies the LayerNorm to the pooled block's tiles as it loads them and
+multiplies them with the Linear's weight (``layer_norm_linear``, after ``layer_norm_stats``). Like the reference's Triton kernels, the pooling and the
 LayerNorm are forward-only (inference).
 
 ``quantize_int8_()`` is the reference's int8 switch (``_USE_INT8_EMB``, online_best/infer.py:893
@@ -20,7 +21,7 @@ from torch import nn
 
 from .layout import pack_slots
 from .ops import (fused_all_slots_embedding, fused_all_slots_embedding_int8, fused_all_slots_embedding_layernorm,
-                  layer_norm, quantize_embedding_int8)
+                  layer_norm, layer_norm_linear, layer_norm_stats, quantize_embedding_int8)
 
 
 class RepEncoder(nn.Module):
@@ -98,4 +99,20 @@ class RepEncoder(nn.Module):
                                                        norm.weight.detach(), norm.bias.detach(), norm.eps)
 
     def forward(self, batch: dict) -> torch.Tensor:
+        """``linear(input_norm(pooled))`` (online_best/infer.py:1029-1085).
+
+        With a bf16 pooled block and a bf16 ``linear`` (the reference's model after
+        ``model.to(bfloat16)``, OB:2797), the LayerNorm statistics are taken over the pooled block
+        and the normalisation runs inside the Linear's matrix-core kernel, so the normalised block
+        never reaches memory; other dtypes normalise with the pooling kernel and run ``linear``.
+        """
+        lin, norm = self.linear, self.input_norm
+        if self.emb.weight.dtype == torch.bfloat16 and lin.weight.dtype == torch.bfloat16 \
+                and norm.weight.dtype in (torch.bfloat16, torch.float32) and norm.weight.dtype == norm.bias.dtype:
+            fused_embs = self.pooled(batch)
+            with torch.no_grad():
+                mean, rstd = layer_norm_stats(fused_embs, norm.eps)
+                return layer_norm_linear(fused_embs, lin.weight.detach(),
+                                         lin.bias.detach() if lin.bias is not None else None, mean=mean, rstd=rstd,
+                                         norm_weight=norm.weight.detach(), norm_bias=norm.bias.detach())
         return self.linear(self.normalized(batch))

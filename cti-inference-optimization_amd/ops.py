@@ -658,3 +658,100 @@ def layer_norm(
             _capi.dtype_code(weight.dtype), float(eps), mean.data_ptr() if mean is not None else None,
             rstd.data_ptr() if rstd is not None else None, _capi.current_stream_handle(dev)))
     return out
+
+
+def layer_norm_stats(x: torch.Tensor, eps: float = 1e-5, mean: Optional[torch.Tensor] = None,
+                     rstd: Optional[torch.Tensor] = None):
+    """Per-row mean and rstd of ``x[rows, cols]`` as the input LayerNorm computes them
+    (online_best/infer.py:843-852, the kernel's M_ptr / R_ptr outputs), without writing the
+    normalised rows. Returns ``(mean, rstd)``, fp32 ``[rows]``."""
+    _require_device_tensor("x", x)
+    dev = x.device
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [rows, cols], got shape {tuple(x.shape)}")
+    _require_contiguous("x", x)
+    rows, cols = x.shape
+    if mean is None:
+        mean = torch.empty(rows, dtype=torch.float32, device=dev)
+    if rstd is None:
+        rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+    for name, t in (("mean", mean), ("rstd", rstd)):
+        _require_device_tensor(name, t, dev)
+        if t.dtype != torch.float32 or t.numel() != rows or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 tensor of {rows} elements")
+    with torch.cuda.device(dev):
+        _capi.check(_capi.lib().cti_ebag_layernorm(
+            x.data_ptr(), None, rows, cols, _capi.dtype_code(x.dtype), None, None, _capi.F32, float(eps),
+            mean.data_ptr(), rstd.data_ptr(), _capi.current_stream_handle(dev)))
+    return mean, rstd
+
+
+def layer_norm_linear(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    mean: Optional[torch.Tensor] = None,
+    rstd: Optional[torch.Tensor] = None,
+    norm_weight: Optional[torch.Tensor] = None,
+    norm_bias: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    out_dtype: Optional[torch.dtype] = None,
+) -> torch.Tensor:
+    """``linear(layer_norm(x))`` of the encoder in one matrix-core kernel
+    (online_best/infer.py:1061-1085): ``x`` bf16 ``[rows, cols]`` (the pooled block), ``mean`` /
+    ``rstd`` fp32 ``[rows]`` (``layer_norm_stats``), ``norm_weight`` / ``norm_bias`` the
+    LayerNorm's gamma / beta ``[cols]`` (fp32 or bf16), ``weight`` / ``bias`` nn.Linear's
+    (bf16 ``[out_features, cols]``, bias fp32 or bf16 ``[out_features]`` or None).
+
+    Each normalised element is computed as the LayerNorm kernel computes it and rounded to bf16
+    as it stores it, then multiplied on the matrix cores with fp32 accumulation; the normalised
+    block never reaches memory. With mean, rstd, norm_weight and norm_bias all None this is the
+    plain Linear. Returns ``out`` ``[rows, out_features]`` (bf16 by default, or ``out_dtype``
+    fp32), written on torch's current stream.
+    """
+    _require_device_tensor("x", x)
+    dev = x.device
+    if x.dim() != 2 or x.dtype != torch.bfloat16:
+        raise ValueError(f"x must be a 2-D bfloat16 tensor, got {tuple(x.shape)} {x.dtype}")
+    _require_contiguous("x", x)
+    rows, cols = x.shape
+    _require_device_tensor("weight", weight, dev)
+    _require_contiguous("weight", weight)
+    if weight.dim() != 2 or weight.shape[1] != cols or weight.dtype != torch.bfloat16:
+        raise ValueError(f"weight must be bfloat16 [out_features, {cols}], got {tuple(weight.shape)} {weight.dtype}")
+    n_out = weight.shape[0]
+    ln_parts = (mean, rstd, norm_weight, norm_bias)
+    ln = any(t is not None for t in ln_parts)
+    if ln and not all(t is not None for t in ln_parts):
+        raise ValueError("mean, rstd, norm_weight and norm_bias must be given together (or none of them)")
+    if ln:
+        for name, t in (("mean", mean), ("rstd", rstd)):
+            _require_device_tensor(name, t, dev)
+            if t.dtype != torch.float32 or t.numel() != rows or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous float32 tensor of {rows} elements")
+        for name, t in (("norm_weight", norm_weight), ("norm_bias", norm_bias)):
+            _require_device_tensor(name, t, dev)
+            _require_contiguous(name, t)
+            if t.numel() != cols or t.dtype not in (torch.float32, torch.bfloat16):
+                raise ValueError(f"{name} must hold {cols} float32 / bfloat16 elements")
+        if norm_weight.dtype != norm_bias.dtype:
+            raise TypeError(f"norm_weight and norm_bias dtypes differ ({norm_weight.dtype} vs {norm_bias.dtype})")
+    if bias is not None:
+        _require_device_tensor("bias", bias, dev)
+        _require_contiguous("bias", bias)
+        if bias.numel() != n_out or bias.dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"bias must hold {n_out} float32 / bfloat16 elements")
+    if out is None:
+        out = torch.empty((rows, n_out), dtype=out_dtype or torch.bfloat16, device=dev)
+    _require_device_tensor("out", out, dev)
+    _require_contiguous("out", out)
+    if out.shape != (rows, n_out) or out.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"out must be [{rows}, {n_out}] float32 / bfloat16, got {tuple(out.shape)} {out.dtype}")
+    ptr = (lambda t: t.data_ptr() if t is not None else None)
+    with torch.cuda.device(dev):
+        _capi.check(_capi.lib().cti_ebag_layernorm_linear(
+            x.data_ptr(), rows, cols, ptr(mean), ptr(rstd), ptr(norm_weight), ptr(norm_bias),
+            _capi.dtype_code(norm_weight.dtype) if ln else _capi.F32, weight.data_ptr(), n_out, ptr(bias),
+            _capi.dtype_code(bias.dtype) if bias is not None else _capi.F32, out.data_ptr(),
+            _capi.dtype_code(out.dtype), _capi.current_stream_handle(dev)))
+    return out

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define CTI_EBAG_ABI_VERSION 3
+#define CTI_EBAG_ABI_VERSION 4
 
 /* element types of tables and outputs */
 #define CTI_EBAG_F32 0
@@ -398,11 +398,35 @@ int cti_ebag_quantize_int8(const void* weight, int32_t dtype, int64_t rows, int6
  *   x, y      [rows, cols] contiguous, element type `dtype` (y may alias x)
  *   gamma     [cols], beta [cols], element type `param_dtype`
  *   mean_out, rstd_out   fp32 [rows] or NULL
+ * y = NULL (with both mean_out and rstd_out given; gamma / beta may then be NULL) writes the
+ * statistics only, the reference kernel's M_ptr / R_ptr outputs (online_best/infer.py:851-852),
+ * for cti_ebag_layernorm_linear.
  * Per-row results are deterministic (fixed reduction order).
  */
 int cti_ebag_layernorm(const void* x, void* y, int64_t rows, int64_t cols, int32_t dtype,
                        const void* gamma, const void* beta, int32_t param_dtype, float eps,
                        float* mean_out, float* rstd_out, void* stream);
+
+/*
+ * The input LayerNorm followed by the encoder's Linear, in one launch on the matrix cores:
+ * replaces `norm_emb = layernorm(fused_embs)` and `rep_emb = self.linear(norm_emb)` at
+ * online_best/infer.py:1061-1085 (nn.Linear(28 * D, d_model), OB:951):
+ *   a[m, k] = bf16( ((x[m, k] - mean[m]) * rstd[m]) * gamma[k] + beta[k] )   (as cti_ebag_layernorm
+ *             computes and stores it, given the same mean / rstd)
+ *   y[m, n] = sum_k a[m, k] * weight[n, k] + bias[n]   (fp32 accumulation, one rounding to y_dtype)
+ *   x        bf16 [rows, cols], 16-byte aligned, cols a multiple of 8
+ *   mean, rstd  fp32 [rows] (from cti_ebag_layernorm with y = NULL, or the pooling pass); with
+ *            mean, rstd, gamma and beta all NULL the kernel is the plain Linear (a = x)
+ *   gamma, beta  [cols], `param_dtype` F32 / BF16, 16-byte aligned
+ *   weight   bf16 [out_features, cols] (nn.Linear's layout), 16-byte aligned
+ *   bias     [out_features] of `bias_dtype` F32 / BF16, or NULL
+ *   y        [rows, out_features] of `y_dtype` F32 / BF16, contiguous
+ * The normalised block is never written to memory. Deterministic (fixed accumulation order).
+ */
+int cti_ebag_layernorm_linear(const void* x, int64_t rows, int32_t cols, const float* mean, const float* rstd,
+                              const void* gamma, const void* beta, int32_t param_dtype, const void* weight,
+                              int32_t out_features, const void* bias, int32_t bias_dtype, void* y,
+                              int32_t y_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,9 @@ CPU restatements of the fused sparse-feature embedding-bag path:
   merge_layouts      online_best/infer.py:581-631 (per-slot concatenation of sub-batches)
   merge_pair_layouts online_best/infer.py:2977-3037 (same, with its int32 round trip)
   layer_norm_np      online_best/infer.py:829-858 (row LayerNorm of the pooled block, fp32)
+  normalize_np       its output step for given per-row mean / rstd
+  layer_norm_linear_np  online_best/infer.py:1061-1085 (the LayerNorm stored in bf16, then the
+                     encoder's Linear in float64)
   quantize_int8_np / quantize_int8_c   online_best/infer.py:895-901 (int8 rows + fp32 scales)
   fma_np             fp32 fused multiply-add emulated exactly in float64 (round to odd)
   bf16 / fp16 encoders and decoders (IEEE round to nearest even)
@@ -419,6 +422,42 @@ def layer_norm_np(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float
     d = (x - mean[:, None]).astype(np.float32)
     var = ((d.astype(np.float64) ** 2).sum(axis=1).astype(np.float32) / n).astype(np.float32)
     rstd = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
-    y = ((d * rstd[:, None]).astype(np.float32) * np.asarray(gamma, np.float32)).astype(np.float32)
-    y = (y + np.asarray(beta, np.float32)).astype(np.float32)
-    return y, mean, rstd
+    return normalize_np(x, mean, rstd, gamma, beta), mean, rstd
+
+
+def normalize_np(x: np.ndarray, mean: np.ndarray, rstd: np.ndarray, gamma: np.ndarray, beta: np.ndarray):
+    """The LayerNorm's output step, online_best/infer.py:855-856, for given per-row mean and rstd:
+    y = ((x - mean) * rstd) * gamma + beta, each operation rounded to fp32 (no fused multiply-add).
+    x float32 [rows, cols]; mean, rstd float32 [rows]; gamma, beta float32 [cols]."""
+    x = np.asarray(x, np.float32)
+    d = (x - np.asarray(mean, np.float32)[:, None]).astype(np.float32)
+    y = ((d * np.asarray(rstd, np.float32)[:, None]).astype(np.float32) * np.asarray(gamma, np.float32))
+    return (y.astype(np.float32) + np.asarray(beta, np.float32)).astype(np.float32)
+
+
+def layer_norm_linear_np(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float, weight: np.ndarray,
+                         bias: Optional[np.ndarray], mean: Optional[np.ndarray] = None,
+                         rstd: Optional[np.ndarray] = None):
+    """online_best/infer.py:1061-1085: the input LayerNorm writes its output into a tensor like
+    the pooled block (bf16 in the reference's model, :1063), and ``self.linear`` maps it to
+    d_model (:1085) with fp32 accumulation and one rounding of the result.
+
+    x float32 [rows, cols] (the bf16 pooled block, decoded); gamma, beta float32 [cols];
+    weight float32 [n, cols] (bf16 values, decoded; nn.Linear's layout); bias float32 [n] or
+    None. mean / rstd: the statistics to normalise with (default: layer_norm_np's).
+    Returns (y, a, absum): y float64 [rows, n] = a @ weight.T + bias summed in float64 (the
+    accumulation order of the reference's GEMM is not observable: comparisons use a bound),
+    a float32 [rows, cols] the normalised rows rounded to bf16, absum float64 [rows, n] =
+    |a| @ |weight|.T (for the fp32 accumulation bound).
+    """
+    if mean is None or rstd is None:
+        y, mean, rstd = layer_norm_np(x, gamma, beta, eps)
+    else:
+        y = normalize_np(x, mean, rstd, gamma, beta)
+    a = decode(encode(y, "bf16"), "bf16")
+    w = np.asarray(weight, np.float64)
+    out = a.astype(np.float64) @ w.T
+    if bias is not None:
+        out = out + np.asarray(bias, np.float64)[None, :]
+    absum = np.abs(a).astype(np.float64) @ np.abs(w).T
+    return out, a, absum

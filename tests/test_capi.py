@@ -24,7 +24,7 @@ def test_header_declares_the_entry_points():
               "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version", "cti_ebag_layernorm",
               "cti_ebag_fused_all_slots_int8", "cti_ebag_quantize_int8", "cti_ebag_fused_all_slots_typed",
               "cti_ebag_narrow_ids", "cti_ebag_stage_copy", "cti_ebag_stage_offset",
-              "cti_ebag_fused_all_slots_layernorm", "cti_ebag_order_bytes"):
+              "cti_ebag_fused_all_slots_layernorm", "cti_ebag_order_bytes", "cti_ebag_layernorm_linear"):
         assert n in names
 
 
@@ -296,6 +296,51 @@ def test_fused_layernorm_python_wrapper_validates_before_any_launch(pkg):
     with pytest.raises(ValueError, match="GPU tensor"):
         pkg.fused_all_slots_embedding_layernorm(z, torch.zeros(2, dtype=torch.int64), torch.zeros(8, dtype=torch.int64),
                                                 w, torch.zeros(3, 64), 3, 32, 9, torch.ones(64), torch.zeros(64))
+
+
+def test_layernorm_linear_rejects_bad_arguments(pkg):
+    """Every case fails a host-side check, so nothing is launched (the pointers are not real)."""
+    c = pkg._capi
+    f = c.lib().cti_ebag_layernorm_linear
+
+    def call(**kw):
+        a = dict(x=256, rows=4, cols=3584, mean=512, rstd=768, gamma=1024, beta=1280, pdt=c.BF16, w=1536, n=512,
+                 bias=2048, bdt=c.BF16, y=4096, ydt=c.BF16)
+        a.update(kw)
+        return f(a["x"], a["rows"], a["cols"], a["mean"], a["rstd"], a["gamma"], a["beta"], a["pdt"], a["w"], a["n"],
+                 a["bias"], a["bdt"], a["y"], a["ydt"], None)
+
+    assert call(rows=-1) == c.EINVAL
+    assert call(cols=0) == c.EINVAL and call(n=0) == c.EINVAL
+    assert call(cols=12) == c.EUNSUPPORTED and "multiple of 8" in c.last_error()
+    assert call(rstd=None) == c.EINVAL and "together" in c.last_error()
+    assert call(pdt=c.F16) == c.EINVAL and call(pdt=c.I8) == c.EINVAL
+    assert call(bdt=c.F16) == c.EINVAL
+    assert call(ydt=c.F16) == c.EINVAL
+    assert call(x=None) == c.EINVAL and call(w=None) == c.EINVAL and call(y=None) == c.EINVAL
+    assert call(x=264) == c.EINVAL and "aligned" in c.last_error()
+    assert call(gamma=1032) == c.EINVAL
+    assert call(rows=2 ** 40) == c.EUNSUPPORTED
+    # nothing to do: no launch, whatever the pointers
+    assert call(rows=0, x=None, w=None, y=None) == c.OK
+
+
+def test_layernorm_statistics_only_needs_both_outputs(pkg):
+    c = pkg._capi
+    f = c.lib().cti_ebag_layernorm
+    #        x    y     rows cols dtype   gamma beta pdt    eps   mean rstd stream
+    assert f(256, None, 4, 64, c.BF16, None, None, c.F32, 1e-5, 512, None, None) == c.EINVAL
+    assert "statistics" in c.last_error()
+    assert f(256, 256, 4, 64, c.BF16, None, 256, c.F32, 1e-5, None, None, None) == c.EINVAL
+
+
+def test_layernorm_linear_python_wrapper_validates_before_any_launch(pkg):
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w = torch.zeros(32, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        pkg.layer_norm_linear(x, w)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        pkg.layer_norm_stats(x)
 
 
 def test_quantize_int8_rejects_bad_arguments(pkg):

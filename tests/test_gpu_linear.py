@@ -1,0 +1,154 @@
+"""The input LayerNorm and the encoder's Linear in one matrix-core kernel (online_best/infer.py:
+1061-1085), through the C ABI, on the GPU.
+
+Bar:
+- integer-valued operands (every product and partial sum exact in fp32): the output equals the
+  exactly computed result rounded once, bit for bit, for the plain Linear and for the LayerNorm
+  path with power-of-two statistics, over tile edges (rows, outputs and K not multiples of the
+  tiles) and both tile shapes;
+- realistic operands: with the kernel's own statistics (cti_ebag_layernorm with no output), the
+  normalised operand is the LayerNorm kernel's bit for bit, so the output must meet the fp32
+  accumulation bound K * 2^-23 * sum|a w| plus the output rounding; against the oracle's own
+  statistics (layer_norm_np, then bf16, then a float64 product) one bf16 ulp per operand more;
+- the statistics match layer_norm_np's; RepEncoder.forward (pooling, statistics, this kernel)
+  matches the oracle's chain pool_c -> layer_norm_np -> bf16 -> Linear.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ebag_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(x, dev):
+    return torch.from_numpy(orc.encode(np.asarray(x, np.float32), "bf16")).view(torch.int16).view(torch.bfloat16).to(dev)
+
+
+def _np(t):
+    t = t.detach().cpu()
+    return t.float().numpy() if t.dtype == torch.bfloat16 else t.numpy()
+
+
+def _exact_round(y64, odt):
+    """The exactly computed result rounded once to the output type (RNE)."""
+    y32 = y64.astype(np.float32)  # exact: integer sums below 2^24
+    assert np.array_equal(y32.astype(np.float64), y64)
+    return y32 if odt == torch.float32 else orc.decode(orc.encode(y32, "bf16"), "bf16")
+
+
+SHAPES = [  # (rows, cols, out_features): tile edges in every dimension, both tile shapes
+    (1, 8, 1), (5, 72, 33), (64, 640, 128), (100, 3584, 200), (300, 136, 512), (4096, 3584, 512),
+    (8192, 896, 512), (129, 14336, 96)]
+
+
+@pytest.mark.parametrize("rows,cols,n", SHAPES)
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float32])
+def test_integer_operands_exact(pkg, dev, rows, cols, n, odt):
+    print(f"linear exact rows={rows} cols={cols} n={n} out={odt}", flush=True)
+    rng = np.random.default_rng(rows + cols + n)
+    x = rng.integers(-1, 2, (rows, cols)).astype(np.float32)
+    w = rng.integers(-1, 2, (n, cols)).astype(np.float32)
+    bias = rng.integers(-8, 9, n).astype(np.float32)
+    got = pkg.layer_norm_linear(_bf16(x, dev), _bf16(w, dev), torch.from_numpy(bias).to(dev), out_dtype=odt)
+    torch.cuda.synchronize()
+    want = _exact_round(x.astype(np.float64) @ w.T.astype(np.float64) + bias, odt)
+    assert np.array_equal(_np(got), want)
+
+
+@pytest.mark.parametrize("rows,cols,n", [(7, 72, 40), (100, 3584, 200), (4096, 3584, 512), (300, 640, 512)])
+@pytest.mark.parametrize("pdt", [torch.bfloat16, torch.float32])
+def test_layer_norm_operands_exact(pkg, dev, rows, cols, n, pdt):
+    """Statistics and parameters that keep the normalised operand exact: x and mean small
+    integers, rstd a power of two, gamma in {1, 2}, beta an integer, so a = ((x - mean) * rstd) *
+    gamma + beta is an integer below 2^8 (exact in bf16) and must land in the right row and
+    column; swapping gamma and beta, or mean and rstd, changes the result."""
+    print(f"ln-linear exact rows={rows} cols={cols} n={n} params={pdt}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = rng.integers(-3, 4, (rows, cols)).astype(np.float32)
+    mean = rng.integers(-2, 3, rows).astype(np.float32)
+    rstd = np.where(rng.random(rows) < 0.5, 1.0, 2.0).astype(np.float32)
+    gamma = rng.integers(1, 3, cols).astype(np.float32)
+    beta = rng.integers(-4, 5, cols).astype(np.float32)
+    w = rng.integers(-1, 2, (n, cols)).astype(np.float32)
+    bias = rng.integers(-8, 9, n).astype(np.float32)
+    a = ((x - mean[:, None]) * rstd[:, None]) * gamma + beta
+    assert np.abs(a).max() < 256
+    to_p = (lambda v: _bf16(v, dev)) if pdt == torch.bfloat16 else (lambda v: torch.from_numpy(v).to(dev))
+    got = pkg.layer_norm_linear(_bf16(x, dev), _bf16(w, dev), _bf16(bias, dev), mean=torch.from_numpy(mean).to(dev),
+                                rstd=torch.from_numpy(rstd).to(dev), norm_weight=to_p(gamma), norm_bias=to_p(beta),
+                                out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    want = a.astype(np.float64) @ w.T.astype(np.float64) + bias
+    assert np.array_equal(_np(got).astype(np.float64), want)
+
+
+def _realistic(rows, cols, n, seed, dev):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = (0.02 * torch.randn(rows, cols, generator=g) + 0.003).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(cols, generator=g)).to(torch.bfloat16)
+    beta = (0.1 * torch.randn(cols, generator=g)).to(torch.bfloat16)
+    w = (torch.randn(n, cols, generator=g) / cols ** 0.5).to(torch.bfloat16)
+    bias = (0.1 * torch.randn(n, generator=g)).to(torch.bfloat16)
+    return [t.to(dev) for t in (x, gamma, beta, w, bias)]
+
+
+@pytest.mark.parametrize("rows,cols,n", [(4096, 3584, 512), (33, 14336, 512), (777, 896, 256)])
+def test_realistic_operands_against_the_oracle(pkg, dev, rows, cols, n):
+    print(f"ln-linear realistic rows={rows} cols={cols} n={n}", flush=True)
+    x, gamma, beta, w, bias = _realistic(rows, cols, n, rows + cols, dev)
+    mean, rstd = pkg.layer_norm_stats(x, 1e-5)
+    y = pkg.layer_norm_linear(x, w, bias, mean=mean, rstd=rstd, norm_weight=gamma, norm_bias=beta)
+    y32 = pkg.layer_norm_linear(x, w, bias, mean=mean, rstd=rstd, norm_weight=gamma, norm_bias=beta,
+                                out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    xn, gn, bn, wn, biasn = (_np(t) for t in (x, gamma, beta, w, bias))
+    # statistics: layer_norm_np's within fp32 summation-order differences
+    _, m_ref, r_ref = orc.layer_norm_np(xn, gn, bn, 1e-5)
+    np.testing.assert_allclose(_np(mean), m_ref, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(_np(rstd), r_ref, rtol=1e-5)
+    # with the kernel's statistics the operand is exact: accumulation and output rounding only
+    ref, a, absum = orc.layer_norm_linear_np(xn, gn, bn, 1e-5, wn, biasn, mean=_np(mean), rstd=_np(rstd))
+    # fp32 accumulation: K additions, each within one fp32 ulp of its partial sum (2^-23 relative,
+    # whatever rounding the matrix cores apply inside an instruction)
+    acc_bound = cols * 2.0 ** -23 * absum
+    assert np.all(np.abs(_np(y32) - ref) <= acc_bound * (1 + 2.0 ** -23) + np.abs(ref) * 2.0 ** -24 + 1e-30)
+    assert np.all(np.abs(_np(y) - ref) <= acc_bound * (1 + 2.0 ** -8) + np.abs(ref) * 2.0 ** -8 + 1e-30)
+    # the bf16 output is the fp32 output rounded once (same accumulation)
+    assert np.array_equal(_np(y), orc.decode(orc.encode(_np(y32), "bf16"), "bf16"))
+    # against the oracle's own statistics: one bf16 ulp per operand more
+    ref2, _, absum2 = orc.layer_norm_linear_np(xn, gn, bn, 1e-5, wn, biasn)
+    tol = np.abs(ref2) * 2.0 ** -8 + (2.0 ** -8 + cols * 2.0 ** -23) * absum2 + 1e-30
+    assert np.all(np.abs(_np(y) - ref2) <= tol)
+    # determinism
+    y_again = pkg.layer_norm_linear(x, w, bias, mean=mean, rstd=rstd, norm_weight=gamma, norm_bias=beta)
+    assert torch.equal(y.view(torch.int16), y_again.view(torch.int16))
+
+
+def test_rep_encoder_forward_against_the_oracle_chain(pkg, dev):
+    """RepEncoder.forward on a bf16 model: pooling, LayerNorm statistics and the fused
+    LayerNorm-Linear, against pool_c -> layer_norm_np -> bf16 -> Linear (float64)."""
+    S, B, D, V, d_model = 28, 200, 128, 5000, 512
+    torch.manual_seed(0)
+    enc = pkg.RepEncoder(V, D, slot_num=S, d_model=d_model).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        enc.emb.weight.normal_(0, 0.02)
+        enc.input_norm.weight.normal_(1, 0.1)
+        enc.input_norm.bias.normal_(0, 0.1)
+    rng = np.random.default_rng(3)
+    lens = rng.integers(0, 14, (S, B))
+    ids = rng.integers(-2, V + 2, int(lens.sum()))
+    ro = np.concatenate([np.concatenate([[0], np.cumsum(l)]) for l in lens]).astype(np.int64)
+    vo = np.concatenate([[0], np.cumsum(lens.sum(axis=1))[:-1]]).astype(np.int64)
+    batch = {"_flat_values": torch.from_numpy(ids).to(dev), "_flat_row_offsets": torch.from_numpy(ro).to(dev),
+             "_val_offsets": torch.from_numpy(vo).to(dev)}
+    y = enc(batch)
+    torch.cuda.synchronize()
+    assert y.shape == (B, d_model) and y.dtype == torch.bfloat16
+    wbits = enc.emb.weight.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+    pooled = orc.decode(orc.pool_c(ids, ro, [wbits] * S, "bf16", "sum", batch=B, val_base=vo), "bf16")
+    ref, _, absum = orc.layer_norm_linear_np(pooled, _np(enc.input_norm.weight), _np(enc.input_norm.bias),
+                                             enc.input_norm.eps, _np(enc.linear.weight), _np(enc.linear.bias))
+    tol = np.abs(ref) * 2.0 ** -8 + (2.0 ** -8 + S * D * 2.0 ** -23) * absum + 1e-30
+    assert np.all(np.abs(_np(y) - ref) <= tol)

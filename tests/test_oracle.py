@@ -360,3 +360,64 @@ def test_layer_norm_planted_mistakes_are_caught():
     no_centre = x / np.sqrt(x.var(axis=1, dtype=np.float64)[:, None] + 1e-5) * g + b
     for wrong in (one_pass, no_centre):
         assert not np.allclose(wrong, ref, rtol=1e-2, atol=1e-2)
+
+
+# ---- input LayerNorm, then the encoder's Linear (online_best/infer.py:1061-1085) ----------------
+def _lin_case(seed, rows=12, cols=448, n=40):
+    x, g, b = _ln_case(seed, rows=rows, cols=cols)
+    rng = np.random.default_rng(seed + 100)
+    w = orc.decode(orc.encode((0.05 * rng.standard_normal((n, cols))).astype(np.float32), "bf16"), "bf16")
+    bias = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    return x, g, b, w, bias
+
+
+def test_layer_norm_linear_matches_torch():
+    """Against torch's own layer_norm and linear in float64 on the same bf16-rounded operands:
+    the oracle's normalised rows are layer_norm_np's, rounded to bf16 (as the reference stores
+    them), and its product is exact up to float64 rounding."""
+    x, g, b, w, bias = _lin_case(1)
+    y, a, absum = orc.layer_norm_linear_np(x, g, b, 1e-5, w, bias)
+    ln = Fn.layer_norm(torch.from_numpy(x).double(), (x.shape[1],), torch.from_numpy(g).double(),
+                       torch.from_numpy(b).double(), 1e-5)
+    a_t = ln.float().to(torch.bfloat16).double()
+    # the fp32 LayerNorm and torch's fp64 one round to the same bf16 value except near a midpoint
+    assert (a_t.numpy() == a).mean() > 0.99
+    ref = Fn.linear(torch.from_numpy(a).double(), torch.from_numpy(w).double(), torch.from_numpy(bias).double())
+    np.testing.assert_allclose(y, ref.numpy(), rtol=1e-12, atol=1e-12)
+    ref_t = Fn.linear(a_t, torch.from_numpy(w).double(), torch.from_numpy(bias).double()).numpy()
+    assert np.all(np.abs(y - ref_t) <= 2.0 ** -8 * absum + 1e-12)  # one bf16 ulp per operand at most
+    assert np.all(absum >= np.abs(y - bias[None, :]) - 1e-12)
+
+
+def test_layer_norm_linear_closed_forms():
+    # weight = the first n rows of the identity: y is the normalised block's first n columns plus
+    # the bias, exactly; a given mean / rstd is used as given
+    x, g, b, _, bias = _lin_case(2, cols=64, n=16)
+    eye = np.eye(16, 64, dtype=np.float32)
+    y, a, _ = orc.layer_norm_linear_np(x, g, b, 1e-5, eye, bias)
+    assert np.array_equal(y, a[:, :16].astype(np.float64) + bias.astype(np.float64))
+    ln, _, _ = orc.layer_norm_np(x, g, b, 1e-5)
+    assert np.array_equal(a, orc.decode(orc.encode(ln, "bf16"), "bf16"))
+    mean = np.full(x.shape[0], 0.5, np.float32)
+    rstd = np.full(x.shape[0], 2.0, np.float32)
+    y2, a2, _ = orc.layer_norm_linear_np(x, g, b, 1e-5, eye, None, mean=mean, rstd=rstd)
+    want = ((x - np.float32(0.5)) * np.float32(2.0)).astype(np.float32) * g + b
+    assert np.array_equal(a2, orc.decode(orc.encode(want.astype(np.float32), "bf16"), "bf16"))
+    assert np.array_equal(y2, a2[:, :16].astype(np.float64))
+
+
+def test_layer_norm_linear_planted_mistakes_are_caught():
+    """The bound the GPU test uses (one bf16 ulp per operand plus fp32 accumulation) rejects a
+    transposed weight, a missing bias, a skipped LayerNorm and gamma / beta swapped."""
+    x, g, b, w, bias = _lin_case(3, cols=64, n=64)
+    y, a, absum = orc.layer_norm_linear_np(x, g, b, 1e-5, w, bias)
+    tol = 2.0 ** -8 * np.abs(y) + (2.0 ** -8 + 64 * 2.0 ** -24) * absum + 1e-12
+
+    def ok(got):
+        return np.all(np.abs(got - y) <= tol)
+
+    assert ok(a.astype(np.float64) @ w.T.astype(np.float64) + bias)
+    assert not ok(a.astype(np.float64) @ w.astype(np.float64) + bias)  # transposed weight
+    assert not ok(a.astype(np.float64) @ w.T.astype(np.float64))  # no bias
+    assert not ok(x.astype(np.float64) @ w.T.astype(np.float64) + bias)  # no LayerNorm
+    assert not ok(orc.layer_norm_linear_np(x, b, g, 1e-5, w, bias)[0])  # gamma / beta swapped
