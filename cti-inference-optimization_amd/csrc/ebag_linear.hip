@@ -10,13 +10,15 @@
 // per-row mean and rstd come from the pooling or statistics pass (cti_ebag_layernorm with no
 // output). Without statistics the kernel is the plain Linear.
 //
-// Mapping: workgroups of 4 wavefronts own a BM x BN tile of y (wavefronts 2 x 2, each
-// (BM/2) x (BN/2)) and walk K in steps of 64: the next step's x and w tiles are loaded into
-// registers while the matrix cores work on the current one from LDS (rows padded to 72
-// elements, so the 16-byte fragment reads of 16 rows hit distinct banks). The products are
-// v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8(l/16) .. +8) and B[8(l/16) .. +8)[l%16]
-// and receives C[4(l/16) + r][l%16], r < 4. Workgroups are numbered so that the tiles of one
-// row band of x run on one XCD (its L2 then serves x's rows to every column tile of the band).
+// Two forms (the products on v_mfma_f32_16x16x32_bf16: lane l supplies A[l%16][8(l/16) .. +8)
+// and B[8(l/16) .. +8)[l%16] and receives C[4(l/16) + r][l%16], r < 4; workgroups numbered so
+// that the tiles of one row band run on one XCD, whose L2 then serves the band to each of them):
+//   ln_linear_big_kernel  K a multiple of 128 (every encoder shape): 128 x 256 or 128 x 128 tiles
+//                         of 8 wavefronts, both operands through LDS;
+//   ln_linear_kernel      any K (a multiple of 8): 64 x 256 tiles of 4 wavefronts, each owning 64
+//                         columns, x through LDS and the weight's fragments straight to registers.
+// Both walk K in steps of 64 with each step's loads issued two steps ahead into rotating register
+// sets, x normalised on its way to LDS, two LDS buffers and one barrier per step.
 #include <stdint.h>
 
 #include "ebag_device.h"
@@ -28,11 +30,11 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kLinThreads = 256;          // 4 wavefronts
-constexpr int kBK = 64;                   // K per step
-constexpr int kLds = kBK + 8;             // LDS row pitch in elements (144 bytes)
-constexpr int kChunks = kBK / 8;          // 16-byte chunks per tile row
+constexpr int kBK = 64;        // K per step
+constexpr int kLds = kBK + 8;  // LDS row pitch in elements (144 bytes)
+constexpr int kChunks = kBK / 8;  // 16-byte chunks per tile row
 constexpr int kXcds = 8;
+constexpr int kWaveCols = 64;  // output columns per wavefront
 
 struct LinearParams {
   const char* x;      // [M, K] bf16
@@ -50,16 +52,6 @@ struct LinearParams {
   int32_t tiles_n;
 };
 
-template <typename PT>
-__device__ __forceinline__ void load_param8(const void* p, int32_t k, bool live, float* out) {
-  if (!live) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = 0.f;
-    return;
-  }
-  load_params<PT, 8>(p, k, out);
-}
-
 // One bf16 chunk (8 elements) normalised: ((x - mean) * rstd) * g + b, rounded to bf16.
 __device__ __forceinline__ uint4 normalise8(const uint4& raw, float mean, float rstd, const float* g, const float* b) {
   float v[8];
@@ -76,15 +68,15 @@ __device__ __forceinline__ void store_y(char* y, int64_t idx, float v) {
   else reinterpret_cast<uint16_t*>(y)[idx] = static_cast<uint16_t>(pack_bf16x2(v, 0.f));
 }
 
-template <int BM, int BN, bool LN, typename PT, typename BT, typename OT>
-__global__ void __launch_bounds__(kLinThreads) ln_linear_kernel(const LinearParams p) {
-  constexpr int WM = BM / 2, WN = BN / 2;     // wavefront tile
-  constexpr int MI = WM / 16, NI = WN / 16;   // 16 x 16 products per wavefront
-  constexpr int PA = BM * kChunks / kLinThreads;  // x chunks per thread and step
-  constexpr int PB = BN * kChunks / kLinThreads;  // w chunks per thread and step
-  static_assert(PA >= 1 && PB >= 1 && MI >= 1 && NI >= 1, "tile shape");
-  __shared__ __align__(16) uint16_t sA[BM * kLds];
-  __shared__ __align__(16) uint16_t sB[BN * kLds];
+template <int BM, int WAVES, int U, bool LN, typename PT, typename BT, typename OT>
+__global__ void __launch_bounds__(WAVES * kWave) ln_linear_kernel(const LinearParams p) {
+  constexpr int THREADS = WAVES * kWave;
+  constexpr int BN = WAVES * kWaveCols;
+  constexpr int MI = BM / 16, NI = kWaveCols / 16;  // 16 x 16 products per wavefront
+  constexpr int PA = BM * kChunks / THREADS;        // x chunks per thread and step
+  constexpr int kRowStep = THREADS / kChunks;
+  static_assert(PA >= 1 && BM * kChunks % THREADS == 0, "tile shape");
+  __shared__ __align__(16) uint16_t sA[2][BM * kLds];
 
   // XCD-contiguous numbering: dispatch position i runs on XCD i % 8; give each XCD a contiguous
   // range of tiles, column tiles fastest, so a row band's tiles share that XCD's L2.
@@ -98,62 +90,99 @@ __global__ void __launch_bounds__(kLinThreads) ln_linear_kernel(const LinearPara
   const int t = static_cast<int>(threadIdx.x);
   const int lane = t & (kWave - 1);
   const int wave = t / kWave;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int kc = t % kChunks;  // this thread's chunk of each tile row (fixed over the K loop)
-  const int r0 = t / kChunks;  // its first tile row; then every kLinThreads / kChunks rows
-  constexpr int kRowStep = kLinThreads / kChunks;
+  const int kc = t % kChunks;  // this thread's chunk of each x row of a step (fixed over K)
+  const int r0 = t / kChunks;  // its first row of the band; then every kRowStep rows
+  const int fr = lane & 15;        // fragment row (A) / column (B)
+  const int fk = (lane >> 4) * 8;  // fragment k offset
 
+  // Every load below reads a valid address (rows past M or N and chunks past K read the last
+  // row / chunk) and its value is replaced by zero afterwards: no branch around a load, so the
+  // loads of a step issue back to back and retire in order.
   float mean[PA], rstd[PA];
+  bool row_ok[PA];
+  const char* xrow[PA];
 #pragma unroll
   for (int q = 0; q < PA; ++q) {
     const int64_t m = m0 + r0 + q * kRowStep;
+    row_ok[q] = m < p.M;
+    const int64_t mc = row_ok[q] ? m : p.M - 1;
     mean[q] = 0.f;
     rstd[q] = 1.f;
     if constexpr (LN) {
-      if (m < p.M) {
-        mean[q] = p.mean[m];
-        rstd[q] = p.rstd[m];
-      }
+      mean[q] = p.mean[mc];
+      rstd[q] = p.rstd[mc];
     }
+    xrow[q] = p.x + mc * p.K * 2;
+  }
+  // this lane's weight rows (one per 16-column fragment of the wavefront)
+  const char* wrow[NI];
+  bool col_ok[NI];
+#pragma unroll
+  for (int c = 0; c < NI; ++c) {
+    const int n = n0 + wave * kWaveCols + c * 16 + fr;
+    col_ok[c] = n < p.N;
+    wrow[c] = p.w + static_cast<int64_t>(col_ok[c] ? n : p.N - 1) * p.K * 2;
   }
 
-  uint4 ra[PA], rb[PB];
-  float g[8], b[8];
   const int nk = (p.K + kBK - 1) / kBK;
-  auto load_step = [&](int ks) {
+  constexpr int PV = LN ? 2 * Elem<PT>::kBytes / 2 : 0;  // 16-byte vectors of gamma + beta per chunk
+  // register sets: step s's x chunks (with their gamma / beta) and weight fragments live in set
+  // s % U from when they are issued (U steps ahead) until they are used
+  uint4 ra[U][PA];
+  uint4 rp[U][PV > 0 ? PV : 1];
+  bf16x8 wb[U][2][NI];
+  const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+  auto issue_x = [&](int ks, uint4 (&a)[PA], uint4 (&pp)[PV > 0 ? PV : 1]) {
     const int k = ks * kBK + kc * 8;
-    const bool kin = k < p.K;
+    const int kq = k < p.K ? k : p.K - 8;  // steps and chunks past K read the last chunk
 #pragma unroll
-    for (int q = 0; q < PA; ++q) {
-      const int64_t m = m0 + r0 + q * kRowStep;
-      ra[q] = (kin && m < p.M) ? load16(p.x + (m * p.K + k) * 2) : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int q = 0; q < PB; ++q) {
-      const int n = n0 + r0 + q * kRowStep;
-      rb[q] = (kin && n < p.N) ? load16(p.w + (static_cast<int64_t>(n) * p.K + k) * 2) : make_uint4(0u, 0u, 0u, 0u);
-    }
+    for (int q = 0; q < PA; ++q) a[q] = load16(xrow[q] + static_cast<int64_t>(kq) * 2);
     if constexpr (LN) {
-      load_param8<PT>(p.gamma, k, kin, g);
-      load_param8<PT>(p.beta, k, kin, b);
+      constexpr int H = Elem<PT>::kBytes / 2;  // 16-byte vectors per 8 parameters
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        pp[h] = load16(static_cast<const char*>(p.gamma) + static_cast<int64_t>(kq) * Elem<PT>::kBytes + h * 16);
+        pp[H + h] = load16(static_cast<const char*>(p.beta) + static_cast<int64_t>(kq) * Elem<PT>::kBytes + h * 16);
+      }
     }
   };
-  auto store_step = [&](int ks) {
-    const int k = ks * kBK + kc * 8;
+  auto issue_w = [&](int ks, bf16x8 (&b)[2][NI]) {
 #pragma unroll
-    for (int q = 0; q < PA; ++q) {
-      const int row = r0 + q * kRowStep;
-      uint4 v = ra[q];
-      if constexpr (LN) {
-        // rows past M and columns past K hold +0 (they must not add beta)
-        if (m0 + row < p.M && k < p.K) v = normalise8(ra[q], mean[q], rstd[q], g, b);
+    for (int h = 0; h < 2; ++h) {
+      const int k = ks * kBK + h * 32 + fk;
+      const int kq = k < p.K ? k : p.K - 8;
+#pragma unroll
+      for (int c = 0; c < NI; ++c) b[h][c] = __builtin_bit_cast(bf16x8, load16(wrow[c] + static_cast<int64_t>(kq) * 2));
+    }
+  };
+  // zero the weight fragments past K or N (after their loads have been waited for)
+  auto mask_w = [&](int ks, bf16x8 (&b)[2][NI]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool kin = ks * kBK + h * 32 + fk < p.K;
+#pragma unroll
+      for (int c = 0; c < NI; ++c)
+        if (!(kin && col_ok[c])) b[h][c] = __builtin_bit_cast(bf16x8, zero4);
+    }
+  };
+  auto put_x = [&](int ks, int buf, const uint4 (&a)[PA], const uint4 (&pp)[PV > 0 ? PV : 1]) {
+    const bool kin = ks * kBK + kc * 8 < p.K;
+    float g[8], bt[8];
+    if constexpr (LN) {
+      constexpr int H = Elem<PT>::kBytes / 2;
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        unpack16(pp[h], g + h * (16 / Elem<PT>::kBytes), PT{});
+        unpack16(pp[H + h], bt + h * (16 / Elem<PT>::kBytes), PT{});
       }
-      *reinterpret_cast<uint4*>(&sA[row * kLds + kc * 8]) = v;
     }
 #pragma unroll
-    for (int q = 0; q < PB; ++q) {
-      const int row = r0 + q * kRowStep;
-      *reinterpret_cast<uint4*>(&sB[row * kLds + kc * 8]) = rb[q];
+    for (int q = 0; q < PA; ++q) {
+      uint4 v = a[q];
+      if constexpr (LN) v = normalise8(a[q], mean[q], rstd[q], g, bt);
+      // rows past M and columns past K hold +0 (they must not add beta)
+      if (!(row_ok[q] && kin)) v = zero4;
+      *reinterpret_cast<uint4*>(&sA[buf][(r0 + q * kRowStep) * kLds + kc * 8]) = v;
     }
   };
 
@@ -162,31 +191,43 @@ __global__ void __launch_bounds__(kLinThreads) ln_linear_kernel(const LinearPara
   for (int a = 0; a < MI; ++a)
 #pragma unroll
     for (int c = 0; c < NI; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  load_step(0);
-  store_step(0);
-  __syncthreads();
-  const int fr = lane & 15;        // fragment row (A) / column (B)
-  const int fk = (lane >> 4) * 8;  // fragment k offset
-  for (int ks = 0; ks < nk; ++ks) {
-    if (ks + 1 < nk) load_step(ks + 1);
+  auto multiply = [&](int buf, const bf16x8 (&b)[2][NI]) {
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += 32) {
-      bf16x8 fa[MI], fb[NI];
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int a = 0; a < MI; ++a)
-        fa[a] = *reinterpret_cast<const bf16x8*>(&sA[(wm * WM + a * 16 + fr) * kLds + kk + fk]);
+      for (int a = 0; a < MI; ++a) {
+        const bf16x8 fa = *reinterpret_cast<const bf16x8*>(&sA[buf][(a * 16 + fr) * kLds + h * 32 + fk]);
 #pragma unroll
-      for (int c = 0; c < NI; ++c)
-        fb[c] = *reinterpret_cast<const bf16x8*>(&sB[(wn * WN + c * 16 + fr) * kLds + kk + fk]);
-#pragma unroll
-      for (int a = 0; a < MI; ++a)
-#pragma unroll
-        for (int c = 0; c < NI; ++c) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[a], fb[c], acc[a][c], 0, 0, 0);
+        for (int c = 0; c < NI; ++c) acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, b[h][c], acc[a][c], 0, 0, 0);
+      }
     }
-    __syncthreads();
-    if (ks + 1 < nk) {
-      store_step(ks + 1);
+  };
+
+  // steps walked: nk rounded up to a multiple of U (the steps past nk load valid addresses and
+  // multiply zeros), so that the unrolled body below holds no branch: the compiler then knows at
+  // every use how many loads were issued after the one it waits for
+  const int nks = (nk + U - 1) / U * U;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    issue_x(u, ra[u], rp[u]);
+    issue_w(u, wb[u]);
+  }
+  put_x(0, 0, ra[0], rp[0]);
+  issue_x(U, ra[0], rp[0]);
+  __syncthreads();
+  // iteration s writes step s + 1's x chunks (set (s + 1) % U) into the other LDS buffer and
+  // refills that set with step s + 1 + U, multiplies step s (LDS buffer s % 2, weight set s % U)
+  // and refills the weight set with step s + U; one barrier per step. The body is unrolled U
+  // times so that every register set keeps its registers across the loop.
+  for (int s0 = 0; s0 < nks; s0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u;
+      put_x(s + 1, (s + 1) & 1, ra[(u + 1) % U], rp[(u + 1) % U]);
+      issue_x(s + 1 + U, ra[(u + 1) % U], rp[(u + 1) % U]);
+      mask_w(s, wb[u]);
+      multiply(s & 1, wb[u]);
+      issue_w(s + U, wb[u]);
       __syncthreads();
     }
   }
@@ -194,7 +235,7 @@ __global__ void __launch_bounds__(kLinThreads) ln_linear_kernel(const LinearPara
   // epilogue: + bias, one rounding to the output type
 #pragma unroll
   for (int c = 0; c < NI; ++c) {
-    const int n = n0 + wn * WN + c * 16 + (lane & 15);
+    const int n = n0 + wave * kWaveCols + c * 16 + fr;
     if (n >= p.N) continue;
     const float bn = p.bias ? Elem<BT>::load(static_cast<const char*>(p.bias) + static_cast<int64_t>(n) * Elem<BT>::kBytes)
                             : 0.f;
@@ -202,30 +243,228 @@ __global__ void __launch_bounds__(kLinThreads) ln_linear_kernel(const LinearPara
     for (int a = 0; a < MI; ++a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t m = m0 + wm * WM + a * 16 + (lane >> 4) * 4 + r;
+        const int64_t m = m0 + a * 16 + (lane >> 4) * 4 + r;
         if (m < p.M) store_y<OT>(p.y, m * p.N + n, acc[a][c][r] + bn);
       }
     }
   }
 }
 
-template <int BM, int BN, bool LN, typename PT, typename BT, typename OT>
-hipError_t launch_tile(LinearParams p, hipStream_t s) {
-  p.tiles_m = static_cast<int32_t>((p.M + BM - 1) / BM);
+// Raw buffer over a whole array: byte offsets (voffset from the lane, soffset from the step).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);  // raw buffer, 32-bit data format
+}
+__device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t voff, uint32_t soff) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// The large form (K a multiple of 128, byte offsets below 2^31): a workgroup of 8 wavefronts
+// (2 x 4, each 64 x BN/4) owns a 128 x BN tile of y (BN = 256, or 128 when that leaves fewer
+// than two tiles per CU); both
+// operands pass through LDS, so each x element loaded feeds BN columns and each weight element
+// 128 rows (the L2 -> CU traffic per product that the matrix cores can sustain). x chunks are
+// normalised on their way to LDS, once per BN columns. Every load reads inside its array (rows
+// past M or N read the last row: their products only reach accumulators that are not stored),
+// buffer loads with the step in the scalar offset, U register sets rotating, two LDS buffers, one
+// barrier per step, no branch in the loop.
+template <int BN, int U, bool LN, typename PT, typename BT, typename OT>
+__global__ void __launch_bounds__(8 * kWave) ln_linear_big_kernel(const LinearParams p) {
+  constexpr int BM = 128, THREADS = 8 * kWave;
+  constexpr int WN = BN / 4;                        // wavefront tile 64 x WN
+  constexpr int MI = 4, NI = WN / 16;
+  constexpr int PA = BM * kChunks / THREADS;        // 2 x chunks per thread and step
+  constexpr int PB = BN * kChunks / THREADS;        // 4 weight chunks
+  constexpr int kRowStep = THREADS / kChunks;       // 64
+  constexpr int PV = LN ? Elem<PT>::kBytes : 0;     // 16-byte vectors of gamma + beta per chunk
+  constexpr int kStageA = BM * kLds, kStageB = BN * kLds;
+  __shared__ __align__(16) uint16_t sA[2][kStageA];
+  __shared__ __align__(16) uint16_t sB[2][kStageB];
+
+  const int total = p.tiles_m * p.tiles_n;
+  const int i = static_cast<int>(blockIdx.x);
+  int tile = i;
+  if (total % kXcds == 0) tile = (i % kXcds) * (total / kXcds) + i / kXcds;
+  const int64_t m0 = static_cast<int64_t>(tile / p.tiles_n) * BM;
+  const int n0 = (tile % p.tiles_n) * BN;
+
+  const int t = static_cast<int>(threadIdx.x);
+  const int lane = t & (kWave - 1);
+  const int wave = t / kWave;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int kc = t % kChunks, r0 = t / kChunks;
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+
+  const Rsrc xr = make_rsrc(p.x, static_cast<uint32_t>(p.M * p.K * 2));
+  const Rsrc wr = make_rsrc(p.w, static_cast<uint32_t>(static_cast<int64_t>(p.N) * p.K * 2));
+  const Rsrc gr = LN ? make_rsrc(p.gamma, static_cast<uint32_t>(p.K * Elem<PT>::kBytes)) : wr;
+  const Rsrc br = LN ? make_rsrc(p.beta, static_cast<uint32_t>(p.K * Elem<PT>::kBytes)) : wr;
+  const uint32_t poff = kc * 8 * Elem<PT>::kBytes;
+  float mean[PA], rstd[PA];
+  uint32_t xoff[PA], woff[PB];
+#pragma unroll
+  for (int q = 0; q < PA; ++q) {
+    const int64_t m = m0 + r0 + q * kRowStep;
+    const int64_t mc = m < p.M ? m : p.M - 1;
+    mean[q] = 0.f;
+    rstd[q] = 1.f;
+    if constexpr (LN) {
+      mean[q] = p.mean[mc];
+      rstd[q] = p.rstd[mc];
+    }
+    xoff[q] = static_cast<uint32_t>((mc * p.K + kc * 8) * 2);
+  }
+#pragma unroll
+  for (int q = 0; q < PB; ++q) {
+    const int n = n0 + r0 + q * kRowStep;
+    woff[q] = static_cast<uint32_t>((static_cast<int64_t>(n < p.N ? n : p.N - 1) * p.K + kc * 8) * 2);
+  }
+
+  const int nk = p.K / kBK;
+  uint4 ra[U][PA], rb[U][PB];
+  uint4 rp[U][PV > 0 ? PV : 1];
+  auto issue = [&](int ks, uint4 (&a)[PA], uint4 (&b)[PB], uint4 (&pp)[PV > 0 ? PV : 1]) {
+    const uint32_t kq = static_cast<uint32_t>(ks < nk ? ks : nk - 1);  // later steps are never used
+#pragma unroll
+    for (int q = 0; q < PA; ++q) a[q] = bload16(xr, xoff[q], kq * kBK * 2);
+    if constexpr (LN) {
+      constexpr int HV = Elem<PT>::kBytes / 2;
+#pragma unroll
+      for (int h = 0; h < HV; ++h) {
+        pp[h] = bload16(gr, poff + h * 16, kq * kBK * Elem<PT>::kBytes);
+        pp[HV + h] = bload16(br, poff + h * 16, kq * kBK * Elem<PT>::kBytes);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < PB; ++q) b[q] = bload16(wr, woff[q], kq * kBK * 2);
+  };
+  auto put = [&](int buf, const uint4 (&a)[PA], const uint4 (&b)[PB], const uint4 (&pp)[PV > 0 ? PV : 1]) {
+    float g[8], bt[8];
+    if constexpr (LN) {
+      constexpr int HV = Elem<PT>::kBytes / 2;
+#pragma unroll
+      for (int h = 0; h < HV; ++h) {
+        unpack16(pp[h], g + h * (16 / Elem<PT>::kBytes), PT{});
+        unpack16(pp[HV + h], bt + h * (16 / Elem<PT>::kBytes), PT{});
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < PA; ++q) {
+      uint4 v = a[q];
+      if constexpr (LN) v = normalise8(a[q], mean[q], rstd[q], g, bt);
+      *reinterpret_cast<uint4*>(&sA[buf][(r0 + q * kRowStep) * kLds + kc * 8]) = v;
+    }
+#pragma unroll
+    for (int q = 0; q < PB; ++q) *reinterpret_cast<uint4*>(&sB[buf][(r0 + q * kRowStep) * kLds + kc * 8]) = b[q];
+  };
+
+  f32x4 acc[MI][NI];
+#pragma unroll
+  for (int a = 0; a < MI; ++a)
+#pragma unroll
+    for (int c = 0; c < NI; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto multiply = [&](int buf) {
+    // every fragment of the step is read first (16 LDS reads in flight), then the products
+    bf16x8 fa[2][MI], fb[2][NI];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int c = 0; c < NI; ++c)
+        fb[h][c] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn * WN + c * 16 + fr) * kLds + h * 32 + fk]);
+#pragma unroll
+      for (int a = 0; a < MI; ++a)
+        fa[h][a] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm * 64 + a * 16 + fr) * kLds + h * 32 + fk]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int a = 0; a < MI; ++a)
+#pragma unroll
+        for (int c = 0; c < NI; ++c)
+          acc[a][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[h][a], fb[h][c], acc[a][c], 0, 0, 0);
+  };
+
+#pragma unroll
+  for (int u = 0; u < U; ++u) issue(u, ra[u], rb[u], rp[u]);
+  put(0, ra[0], rb[0], rp[0]);
+  // kept after the write that reads set 0: hoisted above it, these loads would need registers
+  // of their own, and the loop would begin with copies that wait for every load in flight
+  __builtin_amdgcn_sched_barrier(0);
+  issue(U, ra[0], rb[0], rp[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  // iteration s writes step s + 1 (set (s + 1) % U) into the other LDS buffer and refills that
+  // set with step s + 1 + U, then multiplies step s; nk is a multiple of U, so the unrolled body
+  // holds no branch and each register set keeps its registers across the loop (step nk's write
+  // goes to a buffer that is not read again)
+  for (int s0 = 0; s0 < nk; s0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = s0 + u;
+      put((s + 1) & 1, ra[(u + 1) % U], rb[(u + 1) % U], rp[(u + 1) % U]);
+      // the scheduling barriers keep each phase where it is written: loads moved next to
+      // their use would be waited for at once
+      __builtin_amdgcn_sched_barrier(0);
+      issue(s + 1 + U, ra[(u + 1) % U], rb[(u + 1) % U], rp[(u + 1) % U]);
+      __builtin_amdgcn_sched_barrier(0);
+      multiply(s & 1);
+      __syncthreads();
+    }
+  }
+
+  // epilogue: + bias, one rounding to the output type
+#pragma unroll
+  for (int c = 0; c < NI; ++c) {
+    const int n = n0 + wn * WN + c * 16 + fr;
+    if (n >= p.N) continue;
+    const float bn = p.bias ? Elem<BT>::load(static_cast<const char*>(p.bias) + static_cast<int64_t>(n) * Elem<BT>::kBytes)
+                            : 0.f;
+#pragma unroll
+    for (int a = 0; a < MI; ++a) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + wm * 64 + a * 16 + (lane >> 4) * 4 + r;
+        if (m < p.M) store_y<OT>(p.y, m * p.N + n, acc[a][c][r] + bn);
+      }
+    }
+  }
+}
+
+template <int BN, int U, bool LN, typename PT, typename BT, typename OT>
+hipError_t launch_big(LinearParams p, hipStream_t s) {
+  p.tiles_m = static_cast<int32_t>((p.M + 127) / 128);
   p.tiles_n = (p.N + BN - 1) / BN;
   const int64_t blocks = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
-  hipLaunchKernelGGL((ln_linear_kernel<BM, BN, LN, PT, BT, OT>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kLinThreads), 0, s, p);
+  hipLaunchKernelGGL((ln_linear_big_kernel<BN, U, LN, PT, BT, OT>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(8 * kWave), 0, s, p);
   return hipGetLastError();
 }
 
-// Tile shape by the number of tiles it makes: 128 x 128 when that fills the chip (256 CUs) at
-// least once, else 64 x 128.
+template <int BM, int WAVES, int U, bool LN, typename PT, typename BT, typename OT>
+hipError_t launch_tile(LinearParams p, hipStream_t s) {
+  p.tiles_m = static_cast<int32_t>((p.M + BM - 1) / BM);
+  p.tiles_n = (p.N + WAVES * kWaveCols - 1) / (WAVES * kWaveCols);
+  const int64_t blocks = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
+  hipLaunchKernelGGL((ln_linear_kernel<BM, WAVES, U, LN, PT, BT, OT>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(WAVES * kWave), 0, s, p);
+  return hipGetLastError();
+}
+
+// The large form for K a multiple of 128 with byte offsets below 2^31 (every encoder shape:
+// K = 28 * D): 128 x 256 tiles when there are at least two per CU, else 128 x 128; the general
+// form for the rest.
 template <bool LN, typename PT, typename BT, typename OT>
 hipError_t launch_linear(const LinearParams& p, hipStream_t s) {
-  const int64_t big = ((p.M + 127) / 128) * ((p.N + 127) / 128);
-  if (big >= 256) return launch_tile<128, 128, LN, PT, BT, OT>(p, s);
-  return launch_tile<64, 128, LN, PT, BT, OT>(p, s);
+  const bool big = p.K % (2 * kBK) == 0 && (p.M + 128) * p.K * 2 < (int64_t{1} << 31) &&
+                   static_cast<int64_t>(p.N) * p.K * 2 < (int64_t{1} << 31);
+  if (big) {
+    if ((p.M + 127) / 128 * ((p.N + 255) / 256) >= 2 * 256) return launch_big<256, 2, LN, PT, BT, OT>(p, s);
+    return launch_big<128, 2, LN, PT, BT, OT>(p, s);
+  }
+  return launch_tile<64, 4, 2, LN, PT, BT, OT>(p, s);
 }
 
 template <bool LN, typename PT, typename BT>
@@ -267,7 +506,7 @@ extern "C" int cti_ebag_layernorm_linear(const void* x, int64_t rows, int32_t co
   const auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
   if (!a16(x) || !a16(weight) || (ln && (!a16(gamma) || !a16(beta))))
     return set_error(CTI_EBAG_EINVAL, "x, weight, gamma and beta must be 16-byte aligned");
-  if (rows > (int64_t{INT32_MAX} / 2) * 64 || (rows + 63) / 64 * ((out_features + 127) / 128) > INT32_MAX)
+  if (rows > (int64_t{INT32_MAX} / 2) * 64 || (rows + 63) / 64 * ((out_features + 255) / 256) > INT32_MAX)
     return set_error(CTI_EBAG_EUNSUPPORTED, "%lld rows x %d outputs need too many tiles", (long long)rows, out_features);
   LinearParams p{};
   p.x = static_cast<const char*>(x);

@@ -38,9 +38,12 @@ def _exact_round(y64, odt):
     return y32 if odt == torch.float32 else orc.decode(orc.encode(y32, "bf16"), "bf16")
 
 
-SHAPES = [  # (rows, cols, out_features): tile edges in every dimension, both tile shapes
-    (1, 8, 1), (5, 72, 33), (64, 640, 128), (100, 3584, 200), (300, 136, 512), (4096, 3584, 512),
-    (8192, 896, 512), (129, 14336, 96)]
+SHAPES = [  # (rows, cols, out_features): tile edges in every dimension, every kernel form
+    # K not a multiple of 128: the general form (64 x 256 tiles)
+    (1, 8, 1), (5, 72, 33), (300, 136, 512), (77, 200, 300),
+    # K a multiple of 128: 128 x 128 tiles, and 128 x 256 tiles from two per CU on
+    (64, 640, 128), (100, 3584, 200), (4096, 3584, 512), (8192, 896, 512), (129, 14336, 96),
+    (32768, 256, 512), (40000, 128, 300)]
 
 
 @pytest.mark.parametrize("rows,cols,n", SHAPES)
@@ -57,7 +60,8 @@ def test_integer_operands_exact(pkg, dev, rows, cols, n, odt):
     assert np.array_equal(_np(got), want)
 
 
-@pytest.mark.parametrize("rows,cols,n", [(7, 72, 40), (100, 3584, 200), (4096, 3584, 512), (300, 640, 512)])
+@pytest.mark.parametrize("rows,cols,n", [(7, 72, 40), (100, 3584, 200), (4096, 3584, 512), (300, 640, 512),
+                                         (33000, 256, 512)])
 @pytest.mark.parametrize("pdt", [torch.bfloat16, torch.float32])
 def test_layer_norm_operands_exact(pkg, dev, rows, cols, n, pdt):
     """Statistics and parameters that keep the normalised operand exact: x and mean small
@@ -94,7 +98,8 @@ def _realistic(rows, cols, n, seed, dev):
     return [t.to(dev) for t in (x, gamma, beta, w, bias)]
 
 
-@pytest.mark.parametrize("rows,cols,n", [(4096, 3584, 512), (33, 14336, 512), (777, 896, 256)])
+@pytest.mark.parametrize("rows,cols,n", [(4096, 3584, 512), (33, 14336, 512), (777, 896, 256), (32768, 1024, 512),
+                                         (50, 200, 64)])
 def test_realistic_operands_against_the_oracle(pkg, dev, rows, cols, n):
     print(f"ln-linear realistic rows={rows} cols={cols} n={n}", flush=True)
     x, gamma, beta, w, bias = _realistic(rows, cols, n, rows + cols, dev)
