@@ -29,6 +29,11 @@ torch ops on host tensors there; one kernel over device tensors here) and packin
 (values, offsets) pairs of a bf16-2m batch into the flat layout (online_best/infer.py:960-974,
 two torch.cat and a host list copied to the device there; one kernel here).
 
+`--stage small` times the reference's small-batch call pattern (online_best/infer.py:2849-2863,
+:2689): wall-clock µs per call of the drop-in launch at B in {2, 128, 512, 1024} with length-1
+bags (Python checks included; the raw C call; a HIP-graph replay; RepEncoder.pooled / forward
+on the per-slot batch), and lazy-32k's sub-batches pooled call by call against one merged call.
+
 `--stage layernorm` times the encoder's input LayerNorm instead (online_best/infer.py:1061-1076):
 the workload's batches are pooled once, and each step normalises one pooled block
 [B, sum(D)] (rows/s; roofline bytes = the block read and written plus gamma and beta).
@@ -792,6 +797,142 @@ def bench_layernorm(args, pkg, plan, inputs, wl0, dev):
     print(json.dumps(rec), flush=True)
 
 
+def bench_small(args, pkg, dev):
+    """The reference's small-batch call pattern: _warmup_model drives RepEncoder with per-slot
+    batches of B in {2, 128, 512, 1024} length-1 bags (all ids 1, online_best/infer.py:2849-2863),
+    and grouped serving calls the encoder once per sub-batch (:2689) and concatenates. Per B:
+    wall-clock µs per call (Python argument checks included) of the drop-in launch
+    (fused_all_slots_embedding on the flat layout), of the raw C call with its arguments built
+    once, of a HIP-graph replay of the drop-in launch, of RepEncoder.pooled on the per-slot batch
+    (device packing + launch) and of RepEncoder.forward (pooling, statistics, LayerNorm-Linear);
+    and the GPU time of the launch. Then lazy-32k's 8 sub-batches of 4096: 8 drop-in calls into
+    slices of one output against one call on the merged batch."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    C = pkg._capi
+    lib = C.lib()
+    V, D, S, d_model = 5_000_000, 512, 28, 512
+    log("building RepEncoder(5,000,000, 512, 28 slots, d_model 512) in bf16")
+    torch.manual_seed(0)
+    enc = pkg.RepEncoder(V, D, slot_num=S, d_model=d_model).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        enc.emb.weight.normal_(0.0, 0.01)
+    weight = enc.emb.weight.detach()
+    n_calls = max(args.steps, 50)
+
+    def wall(fn, n=n_calls):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e6
+
+    def gpu(fn, n=n_calls):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    per_b = {}
+    for B in (2, 128, 512, 1024):
+        offs = torch.arange(B + 1, dtype=torch.long, device=dev)
+        vals = torch.ones(B, dtype=torch.long, device=dev)
+        slot_batch = {s: (vals, offs) for s in range(1, S + 1)}
+        flat = pkg.pack_slots([slot_batch[s] for s in range(1, S + 1)])
+        fv, vo, ro = flat["_flat_values"], flat["_val_offsets"], flat["_flat_row_offsets"]
+        out = torch.empty((B, S * D), dtype=weight.dtype, device=dev)
+
+        def drop_in():
+            pkg.fused_all_slots_embedding(fv, vo, ro, weight, out, B, D, V - 1)
+
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        raw_args = (fv.data_ptr(), vo.data_ptr(), ro.data_ptr(), weight.data_ptr(), C.BF16, out.data_ptr(), B, S, D,
+                    V - 1, fv.numel(), stream)
+
+        def raw():
+            C.check(lib.cti_ebag_fused_all_slots(*raw_args))
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            drop_in()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            drop_in()
+        torch.cuda.synchronize()
+        want = out.clone()
+        rec = {"drop_in_call_us": wall(drop_in), "raw_c_call_us": wall(raw), "graph_replay_us": wall(graph.replay),
+               "rep_encoder_pooled_us": wall(lambda: enc.pooled(slot_batch)),
+               "rep_encoder_forward_us": wall(lambda: enc(slot_batch)),
+               "launch_gpu_us": gpu(drop_in)}
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(out.view(torch.int16), want.view(torch.int16)):
+            raise RuntimeError(f"B={B}: the graph replay differs from the eager launch")
+        per_b[B] = rec
+        log(f"B={B}: " + ", ".join(f"{k} {v:.1f}" for k, v in rec.items()))
+        del graph
+
+    log("lazy-32k sub-batches: 8 calls into one output against one call on the merged batch")
+    lazy = pkg.workloads.make("lazy-32k", seed=1, vocab=V)
+    subs = []
+    for sb in lazy.sub_batches:
+        ro_s = np.concatenate([sb.offsets[f * sb.batch:(f + 1) * sb.batch + 1] - sb.offsets[f * sb.batch]
+                               for f in range(S)]).astype(np.int64)
+        subs.append((torch.from_numpy(sb.values).to(dev), torch.from_numpy(sb.offsets[0:S * sb.batch:sb.batch].copy()).to(dev),
+                     torch.from_numpy(ro_s).to(dev), sb.batch))
+    merged = pkg.merge_batches([{"_flat_values": v, "_val_offsets": o, "_flat_row_offsets": r} for v, o, r, _ in subs], S)
+    Bm = lazy.batch
+    out_m = torch.empty((Bm, S * D), dtype=weight.dtype, device=dev)
+    out_s = torch.empty_like(out_m)
+
+    def per_sub():
+        row = 0
+        for v, o, r, b in subs:
+            pkg.fused_all_slots_embedding(v, o, r, weight, out_s[row:row + b], b, D, V - 1)
+            row += b
+
+    def one_merged():
+        pkg.fused_all_slots_embedding(merged["_flat_values"], merged["_val_offsets"], merged["_flat_row_offsets"],
+                                      weight, out_m, Bm, D, V - 1)
+
+    sub_rec = {"per_sub_batch_calls_us": wall(per_sub, 20), "merged_call_us": wall(one_merged, 20),
+               "per_sub_batch_gpu_us": gpu(per_sub, 20), "merged_gpu_us": gpu(one_merged, 20)}
+    per_sub()
+    one_merged()
+    torch.cuda.synchronize()
+    if not torch.equal(out_s.view(torch.int16), out_m.view(torch.int16)):
+        raise RuntimeError("per-sub-batch pooling differs from the merged batch's")
+    log("sub-batches: " + ", ".join(f"{k} {v:.1f}" for k, v in sub_rec.items()))
+    ref = per_b[128]
+    rec = {
+        "metric": "drop-in pooling calls/sec at the reference's warmup batch sizes (B=128 shown; "
+                  "one shared bf16 [5e6, 512] table, 28 slots, length-1 bags)",
+        "value": 1e6 / ref["drop_in_call_us"], "unit": "calls/s", "n_gpus": 1, "steps": n_calls, "warmup": 10,
+        "ms_per_step": ref["drop_in_call_us"] / 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: per-slot batches of length-1 bags with id 1 (as online_best/infer.py:2849-2863); "
+                "lazy-32k sub-batches (seed 1)",
+        "config": {"workload": "reference warmup batches B in {2, 128, 512, 1024}; lazy-32k's 8 sub-batches of 4096"},
+        "us_per_call": {str(k): v for k, v in per_b.items()}, "sub_batches": sub_rec,
+        "roofline": None, "cpu_baseline": None,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main_kernel_name(wl, args):
     """The pooling launch sequence's kernels: fields of several row widths share one mixed-width
     launch sequence; binning adds its pass and the list kernel."""
@@ -821,7 +962,8 @@ def main():
     ap.add_argument("--bins", action="store_true", help="run the device length-binning pass")
     ap.add_argument("--block-threshold", type=int, default=0)
     ap.add_argument("--split-threshold", type=int, default=0)
-    ap.add_argument("--stage", default="pool", choices=["pool", "layernorm", "h2d", "encoder", "layout", "reference"],
+    ap.add_argument("--stage", default="pool",
+                    choices=["pool", "layernorm", "h2d", "encoder", "layout", "reference", "small"],
                     help="time the pooling step (default), the input LayerNorm over pooled blocks, or the "
                          "step end to end from host batches")
     ap.add_argument("--int8", action="store_true", help="int8 row-quantised tables (quantised on the device)")
@@ -873,6 +1015,8 @@ def main():
         return bench_layout(args, pkg, dev)
     if args.stage == "reference":
         return bench_reference(args, pkg, dev)
+    if args.stage == "small":
+        return bench_small(args, pkg, dev)
     log(f"workload {args.workload}: generating {args.sets} index sets")
     wls = [W.make(args.workload, seed=s) for s in range(1, args.sets + 1)]
     wl0 = wls[0]
