@@ -679,14 +679,21 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, Rsrc
   load_chunk(raw, 0);
   load_chunk(raw_next, kWave);
   unsigned int ids = (lane < T ? static_cast<unsigned int>(clamp_i64(raw.value(), 0, max_row)) : r_pad) << shift;
+  // int8 rows: the scales of a chunk's rows, one per lane, loaded when the chunk's ids are taken
+  // (pad rows read zeros past the scales); a row's scale is read with readlane when it is added.
+  // sc_issue: the chunk being issued; sc_add: the chunk of the rows being added (the previous
+  // one for a step, after the issue has moved on to a new chunk)
+  float sc_issue = 0.f, sc_add = 0.f;
+  if constexpr (Q) {
+    sc_issue = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, ids >> sshift, 0, 0));
+    sc_add = sc_issue;
+  }
 
   uint32_t v[K];
-  float sc[K] = {};  // int8 rows: each row's scale, loaded with it (unused otherwise)
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const unsigned int r = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), k));
     v[k] = load_lane<BPL>(rsrc, r + lane_off);
-    if constexpr (Q) sc[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, r >> sshift, 0, 0));
   }
 
   float acc[E];
@@ -725,10 +732,15 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, Rsrc
   int j = 0;
   for (; j + K <= T; j += K) {
     const int c_issue = (j + K) & (kWave - 1);  // lane of walk row j + K in its id chunk
+    const int c_add = j & (kWave - 1);          // lane of walk row j in its id chunk
+    if constexpr (Q) {
+      if (c_add == 0) sc_add = sc_issue;  // the rows added now are in the chunk issued since
+    }
     if (c_issue == 0) {
       // rows j + K .. are in the next chunk: take it, and load the one after it
       ids = (j + K + lane < T ? static_cast<unsigned int>(clamp_i64(raw_next.value(), 0, max_row)) : r_pad) << shift;
       load_chunk(raw_next, j + K + kWave);
+      if constexpr (Q) sc_issue = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, ids >> sshift, 0, 0));
     }
     int dn = next_end - j - 1;  // step row after which the next bag ends
     unsigned int roff[K];       // this step's row offsets, uniform (scalar registers)
@@ -737,21 +749,28 @@ __device__ __forceinline__ void stream_walk(const PoolParams& p, Rsrc rsrc, Rsrc
       roff[k] = static_cast<unsigned int>(__builtin_amdgcn_readlane(static_cast<int>(ids), c_issue + k));
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      acc_lane<TT, BPL>(acc, v[k], sc[k]);
+      float s = 0.f;
+      if constexpr (Q) s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_add), c_add + k));
+      acc_lane<TT, BPL>(acc, v[k], s);
       if (k == dn) {
         flush(j + k + 1);
         dn = next_end - j - 1;
       }
       v[k] = load_lane<BPL>(rsrc, roff[k] + lane_off);
-      if constexpr (Q) sc[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, roff[k] >> sshift, 0, 0));
     }
   }
   if (j < T) {  // the partial last step: rows j .. T - 1, nothing issued
+    const int c_add = j & (kWave - 1);
+    if constexpr (Q) {
+      if (c_add == 0) sc_add = sc_issue;
+    }
     int dn = next_end - j - 1;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       if (j + k < T) {
-        acc_lane<TT, BPL>(acc, v[k], sc[k]);
+        float s = 0.f;
+        if constexpr (Q) s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc_add), c_add + k));
+        acc_lane<TT, BPL>(acc, v[k], s);
         if (k == dn) {
           flush(j + k + 1);
           dn = next_end - j - 1;
