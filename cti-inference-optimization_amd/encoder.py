@@ -5,10 +5,11 @@ names, forward(batch) contract): the 28 slots are pooled into ``[B, slot_num*emb
 table's dtype and normalised with the ``input_norm`` parameters (the reference's Triton
 LayerNorm, online_best/infer.py:1061-1076) by one fused kernel
 (``fused_all_slots_embedding_layernorm``; ``pooled`` alone uses ``fused_all_slots_embedding``),
-and ``linear`` maps them to d_model (online_best/infer.py:1085): for the bf16 model, one
-matrix-core kernel applies the LayerNorm to the pooled block's tiles as it loads them and
-multiplies them with the Linear's weight (``layer_norm_linear``, after ``layer_norm_stats``). Like the reference's Triton kernels, the pooling and the
-LayerNorm are forward-only (inference).
+and ``linear`` maps them to d_model (online_best/infer.py:1085). ``forward`` pools, normalises
+the pooled block in place and runs ``linear``; ``forward(batch, fused_linear=True)`` instead runs
+one matrix-core kernel that applies the LayerNorm to the pooled block's tiles as it loads them
+and multiplies them with the Linear's weight (``layer_norm_linear``, after ``layer_norm_stats``).
+Like the reference's Triton kernels, the pooling and the LayerNorm are forward-only (inference).
 
 ``quantize_int8_()`` is the reference's int8 switch (``_USE_INT8_EMB``, online_best/infer.py:893
 and :976-1026): the table is row-quantised once on the device and every later ``pooled`` reads
@@ -98,21 +99,31 @@ class RepEncoder(nn.Module):
                                                        batch_size, self.emb_dim, self.emb.num_embeddings - 1,
                                                        norm.weight.detach(), norm.bias.detach(), norm.eps)
 
-    def forward(self, batch: dict) -> torch.Tensor:
+    def forward(self, batch: dict, fused_linear: bool = False) -> torch.Tensor:
         """``linear(input_norm(pooled))`` (online_best/infer.py:1029-1085).
 
-        With a bf16 pooled block and a bf16 ``linear`` (the reference's model after
-        ``model.to(bfloat16)``, OB:2797), the LayerNorm statistics are taken over the pooled block
-        and the normalisation runs inside the Linear's matrix-core kernel, so the normalised block
-        never reaches memory; other dtypes normalise with the pooling kernel and run ``linear``.
+        By default the pooled block is normalised in place by the LayerNorm kernel and mapped by
+        ``linear`` (torch's GEMM), the fastest order measured at every timed shape: the encoder
+        shape (B = 4096, Linear 3584 -> 512), the merged 32,768-sample batch, and the reference's
+        small batches (where the library GEMM splits K over the chip). ``fused_linear=True`` takes
+        the statistics pass and the matrix-core kernel that normalises the pooled block's tiles as
+        it loads them (``layer_norm_linear``), so the normalised block never reaches memory; it
+        needs a bf16 table and a bf16 ``linear`` with LayerNorm parameters in bf16 or fp32 (the
+        reference's model after ``model.to(bfloat16)``, online_best/infer.py:2797).
         """
         lin, norm = self.linear, self.input_norm
-        if self.emb.weight.dtype == torch.bfloat16 and lin.weight.dtype == torch.bfloat16 \
-                and norm.weight.dtype in (torch.bfloat16, torch.float32) and norm.weight.dtype == norm.bias.dtype:
+        if fused_linear:
+            if not (self.emb.weight.dtype == torch.bfloat16 and lin.weight.dtype == torch.bfloat16
+                    and norm.weight.dtype in (torch.bfloat16, torch.float32) and norm.weight.dtype == norm.bias.dtype
+                    and self._int8_weight is None):
+                raise ValueError("fused_linear needs a bf16 table and Linear and bf16 or fp32 LayerNorm parameters")
             fused_embs = self.pooled(batch)
             with torch.no_grad():
                 mean, rstd = layer_norm_stats(fused_embs, norm.eps)
                 return layer_norm_linear(fused_embs, lin.weight.detach(),
                                          lin.bias.detach() if lin.bias is not None else None, mean=mean, rstd=rstd,
                                          norm_weight=norm.weight.detach(), norm_bias=norm.bias.detach())
-        return self.linear(self.normalized(batch))
+        fused_embs = self.pooled(batch)
+        with torch.no_grad():
+            fused_embs = layer_norm(fused_embs, norm.weight.detach(), norm.bias.detach(), norm.eps, out=fused_embs)
+        return self.linear(fused_embs)

@@ -10,8 +10,9 @@ Bar:
   normalised operand is the LayerNorm kernel's bit for bit, so the output must meet the fp32
   accumulation bound K * 2^-23 * sum|a w| plus the output rounding; against the oracle's own
   statistics (layer_norm_np, then bf16, then a float64 product) one bf16 ulp per operand more;
-- the statistics match layer_norm_np's; RepEncoder.forward (pooling, statistics, this kernel)
-  matches the oracle's chain pool_c -> layer_norm_np -> bf16 -> Linear.
+- the statistics match layer_norm_np's; RepEncoder.forward, with this kernel or with the
+  LayerNorm kernel and torch's Linear, matches the oracle's chain pool_c -> layer_norm_np -> bf16
+  -> Linear.
 """
 import numpy as np
 import pytest
@@ -132,8 +133,9 @@ def test_realistic_operands_against_the_oracle(pkg, dev, rows, cols, n):
 
 
 def test_rep_encoder_forward_against_the_oracle_chain(pkg, dev):
-    """RepEncoder.forward on a bf16 model: pooling, LayerNorm statistics and the fused
-    LayerNorm-Linear, against pool_c -> layer_norm_np -> bf16 -> Linear (float64)."""
+    """RepEncoder.forward on a bf16 model, in both orders (pooling, the LayerNorm kernel and
+    torch's Linear; pooling, statistics and the fused LayerNorm-Linear), against pool_c ->
+    layer_norm_np -> bf16 -> Linear (float64)."""
     S, B, D, V, d_model = 28, 200, 128, 5000, 512
     torch.manual_seed(0)
     enc = pkg.RepEncoder(V, D, slot_num=S, d_model=d_model).to(dev).to(torch.bfloat16)
@@ -148,12 +150,17 @@ def test_rep_encoder_forward_against_the_oracle_chain(pkg, dev):
     vo = np.concatenate([[0], np.cumsum(lens.sum(axis=1))[:-1]]).astype(np.int64)
     batch = {"_flat_values": torch.from_numpy(ids).to(dev), "_flat_row_offsets": torch.from_numpy(ro).to(dev),
              "_val_offsets": torch.from_numpy(vo).to(dev)}
-    y = enc(batch)
-    torch.cuda.synchronize()
-    assert y.shape == (B, d_model) and y.dtype == torch.bfloat16
     wbits = enc.emb.weight.detach().cpu().view(torch.int16).numpy().view(np.uint16)
     pooled = orc.decode(orc.pool_c(ids, ro, [wbits] * S, "bf16", "sum", batch=B, val_base=vo), "bf16")
     ref, _, absum = orc.layer_norm_linear_np(pooled, _np(enc.input_norm.weight), _np(enc.input_norm.bias),
                                              enc.input_norm.eps, _np(enc.linear.weight), _np(enc.linear.bias))
+    # one bf16 ulp per operand and of the output, plus fp32 accumulation over K
     tol = np.abs(ref) * 2.0 ** -8 + (2.0 ** -8 + S * D * 2.0 ** -23) * absum + 1e-30
-    assert np.all(np.abs(_np(y) - ref) <= tol)
+    for fused_linear in (False, True):
+        y = enc(batch, fused_linear=fused_linear)
+        torch.cuda.synchronize()
+        assert y.shape == (B, d_model) and y.dtype == torch.bfloat16
+        assert np.all(np.abs(_np(y) - ref) <= tol), fused_linear
+    enc.float()
+    with pytest.raises(ValueError, match="fused_linear"):
+        enc(batch, fused_linear=True)
