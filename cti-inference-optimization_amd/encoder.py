@@ -57,7 +57,9 @@ class RepEncoder(nn.Module):
             slots = []
             for i in range(self.slot_num):
                 vals, offs = batch[i + 1]
-                slots.append((vals.to(device), offs.to(device)))
+                # tensors already on a GPU are passed as they are (pack_slots checks that they are
+                # on this one): .to() on them costs as much as the rest of the packing
+                slots.append((vals if vals.is_cuda else vals.to(device), offs if offs.is_cuda else offs.to(device)))
             batch = pack_slots(slots)
         flat_values = batch["_flat_values"]
         flat_row_offsets = batch["_flat_row_offsets"]

@@ -102,18 +102,21 @@ def pack_slots(slots: Sequence[Tuple[torch.Tensor, torch.Tensor]], with_global_o
     if not slots:
         raise ValueError("no slots to pack")
     dev = slots[0][0].device
+    if dev.type != "cuda":
+        raise ValueError(f"slot 0: all tensors must be on the same GPU ({dev})")
+    di = dev.index if dev.index is not None else torch.cuda.current_device()
     batch_size = slots[0][1].numel() - 1
-    vals, offs = [], []
-    for s, (v, o) in enumerate(slots):
-        if v.device != dev or o.device != dev or dev.type != "cuda":
+    vals, offs, nnz = [], [], []
+    for s, (v, o) in enumerate(slots):  # few tensor attributes per slot: they dominate small calls
+        if v.get_device() != di or o.get_device() != di:
             raise ValueError(f"slot {s}: all tensors must be on the same GPU ({dev})")
-        if v.dtype != torch.int64 or o.dtype != torch.int64:
+        if v.dtype is not torch.int64 or o.dtype is not torch.int64:
             raise TypeError(f"slot {s}: values and offsets must be int64")
         if o.numel() != batch_size + 1:
             raise ValueError(f"slot {s}: offsets has {o.numel()} entries, expected {batch_size + 1}")
-        vals.append(v.contiguous())
-        offs.append(o.contiguous())
-    nnz = [v.numel() for v in vals]
+        vals.append(v if v.is_contiguous() else v.contiguous())
+        offs.append(o if o.is_contiguous() else o.contiguous())
+        nnz.append(v.numel())
     total = sum(nnz)
     S = len(slots)
     flat_values = torch.empty(total, dtype=torch.int64, device=dev)

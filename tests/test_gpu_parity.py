@@ -381,6 +381,23 @@ def test_pack_slots_matches_restatement(pkg, dev):
     assert np.array_equal(got["_flat_row_offsets"].cpu().numpy(), fro)
     assert np.array_equal(got["_val_offsets"].cpu().numpy(), fvo)
     assert np.array_equal(got["offsets"].cpu().numpy(), orc.to_global_offsets(fvo, fro, case.B, len(fv)))
+    # non-contiguous slot tensors are packed from a contiguous copy
+    strided = [(torch.from_numpy(np.repeat(v, 2)).to(dev)[::2], torch.from_numpy(o).to(dev)) for v, o in slots]
+    assert any(not t.is_contiguous() for t, _ in strided)
+    again = pkg.pack_slots(strided)
+    assert np.array_equal(again["_flat_values"].cpu().numpy(), fv)
+
+
+def test_pack_slots_rejects_bad_slots(pkg, dev):
+    v, o = torch.arange(3, device=dev), torch.tensor([0, 1, 3], device=dev)
+    with pytest.raises(ValueError, match="same GPU"):
+        pkg.pack_slots([(v, o), (v.cpu(), o)])
+    with pytest.raises(ValueError, match="same GPU"):
+        pkg.pack_slots([(v.cpu(), o.cpu())])
+    with pytest.raises(TypeError, match="int64"):
+        pkg.pack_slots([(v, o), (v.int(), o)])
+    with pytest.raises(ValueError, match="entries"):
+        pkg.pack_slots([(v, o), (v, o[:2])])
 
 
 def test_merge_batches_matches_restatement_and_pooling_commutes(pkg, dev):
