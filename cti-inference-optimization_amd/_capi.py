@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must precede the dlopen below, see module docstring
 LIB_NAME = "libcti_ebag.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, BF16, F16, I8 = 0, 1, 2, 3
 I64, I32 = 0, 1
@@ -109,8 +109,9 @@ SIGNATURES = {
     ),
     "cti_ebag_layernorm_linear": (
         ctypes.c_int,
-        [_P, _I64, _I32, _P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P],
+        [_P, _I64, _I32, _P, _P, _P, _P, _I32, _P, _I32, _P, _I32, _P, _I32, _P, _I64, _P],
     ),
+    "cti_ebag_layernorm_linear_workspace_bytes": (ctypes.c_int64, [_I64, _I32, _I32]),
     "cti_ebag_fused_all_slots_int8": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _I32, _I64, _I32, _I32, _I64, _I64, _P],

@@ -18,7 +18,10 @@
 //   ln_linear_kernel      any K (a multiple of 8): 64 x 256 tiles of 4 wavefronts, each owning 64
 //                         columns, x through LDS and the weight's fragments straight to registers.
 // Both walk K in steps of 64 with each step's loads issued two steps ahead into rotating register
-// sets, x normalised on its way to LDS, two LDS buffers and one barrier per step.
+// sets, x normalised on its way to LDS, two LDS buffers and one barrier per step. When the large
+// form's tiles would leave CUs idle (few rows), K is split over several workgroups per tile: each
+// writes its fp32 partial products to a caller's workspace and ln_linear_reduce_kernel adds the
+// splits in split order, adds the bias and rounds once.
 #include <stdint.h>
 
 #include "ebag_device.h"
@@ -35,6 +38,7 @@ constexpr int kLds = kBK + 8;  // LDS row pitch in elements (144 bytes)
 constexpr int kChunks = kBK / 8;  // 16-byte chunks per tile row
 constexpr int kXcds = 8;
 constexpr int kWaveCols = 64;  // output columns per wavefront
+constexpr int64_t kSplitTarget = 256;  // split K until the large form has one workgroup per CU
 
 struct LinearParams {
   const char* x;      // [M, K] bf16
@@ -50,6 +54,8 @@ struct LinearParams {
   int32_t K;
   int32_t tiles_m;
   int32_t tiles_n;
+  float* part;          // split K: fp32 partial products [splits, M, N] (no bias), NULL: no split
+  int32_t split_steps;  // split K: steps of kBK per split (even); split s is blockIdx.y
 };
 
 // One bf16 chunk (8 elements) normalised: ((x - mean) * rstd) * g + b, rounded to bf16.
@@ -323,11 +329,14 @@ __global__ void __launch_bounds__(8 * kWave) ln_linear_big_kernel(const LinearPa
     woff[q] = static_cast<uint32_t>((static_cast<int64_t>(n < p.N ? n : p.N - 1) * p.K + kc * 8) * 2);
   }
 
-  const int nk = p.K / kBK;
+  // this workgroup's steps of K: all of them, or split blockIdx.y's range (an even count)
+  const int nk_all = p.K / kBK;
+  const int ks0 = p.part ? static_cast<int>(blockIdx.y) * p.split_steps : 0;
+  const int nk = p.part ? (nk_all - ks0 < p.split_steps ? nk_all - ks0 : p.split_steps) : nk_all;
   uint4 ra[U][PA], rb[U][PB];
   uint4 rp[U][PV > 0 ? PV : 1];
   auto issue = [&](int ks, uint4 (&a)[PA], uint4 (&b)[PB], uint4 (&pp)[PV > 0 ? PV : 1]) {
-    const uint32_t kq = static_cast<uint32_t>(ks < nk ? ks : nk - 1);  // later steps are never used
+    const uint32_t kq = static_cast<uint32_t>(ks0 + (ks < nk ? ks : nk - 1));  // later steps are never used
 #pragma unroll
     for (int q = 0; q < PA; ++q) a[q] = bload16(xr, xoff[q], kq * kBK * 2);
     if constexpr (LN) {
@@ -415,6 +424,23 @@ __global__ void __launch_bounds__(8 * kWave) ln_linear_big_kernel(const LinearPa
     }
   }
 
+  if (p.part) {  // split K: this split's fp32 partial products, added up by the reduction kernel
+    float* const part = p.part + static_cast<int64_t>(blockIdx.y) * p.M * p.N;
+#pragma unroll
+    for (int c = 0; c < NI; ++c) {
+      const int n = n0 + wn * WN + c * 16 + fr;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int a = 0; a < MI; ++a) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = m0 + wm * 64 + a * 16 + (lane >> 4) * 4 + r;
+          if (m < p.M) part[m * p.N + n] = acc[a][c][r];
+        }
+      }
+    }
+    return;
+  }
   // epilogue: + bias, one rounding to the output type
 #pragma unroll
   for (int c = 0; c < NI; ++c) {
@@ -433,13 +459,33 @@ __global__ void __launch_bounds__(8 * kWave) ln_linear_big_kernel(const LinearPa
   }
 }
 
+// Split K: y[m, n] = (sum over splits, in split order, of the fp32 partials) + bias, one rounding.
+template <typename BT, typename OT>
+__global__ void __launch_bounds__(256) ln_linear_reduce_kernel(const LinearParams p, int32_t splits) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= p.M * p.N) return;
+  const int n = static_cast<int>(i % p.N);
+  float v = p.part[i];
+  for (int sp = 1; sp < splits; ++sp) v += p.part[static_cast<int64_t>(sp) * p.M * p.N + i];
+  const float bn = p.bias ? Elem<BT>::load(static_cast<const char*>(p.bias) + static_cast<int64_t>(n) * Elem<BT>::kBytes)
+                          : 0.f;
+  store_y<OT>(p.y, i, v + bn);
+}
+
 template <int BN, int U, bool LN, typename PT, typename BT, typename OT>
-hipError_t launch_big(LinearParams p, hipStream_t s) {
+hipError_t launch_big(LinearParams p, int splits, hipStream_t s) {
   p.tiles_m = static_cast<int32_t>((p.M + 127) / 128);
   p.tiles_n = (p.N + BN - 1) / BN;
   const int64_t blocks = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
-  hipLaunchKernelGGL((ln_linear_big_kernel<BN, U, LN, PT, BT, OT>), dim3(static_cast<unsigned>(blocks)),
+  if (splits <= 1) p.part = nullptr;
+  hipLaunchKernelGGL((ln_linear_big_kernel<BN, U, LN, PT, BT, OT>),
+                     dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(splits > 1 ? splits : 1)),
                      dim3(8 * kWave), 0, s, p);
+  if (splits > 1) {
+    const int64_t n = p.M * p.N;
+    hipLaunchKernelGGL((ln_linear_reduce_kernel<BT, OT>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                       s, p, splits);
+  }
   return hipGetLastError();
 }
 
@@ -453,28 +499,55 @@ hipError_t launch_tile(LinearParams p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// The large form for K a multiple of 128 with byte offsets below 2^31 (every encoder shape:
-// K = 28 * D): 128 x 256 tiles when there are at least two per CU, else 128 x 128; the general
-// form for the rest.
+// The large form applies to K a multiple of 128 with byte offsets below 2^31 (every encoder shape:
+// K = 28 * D).
+bool big_form(int64_t M, int32_t N, int32_t K) {
+  return K % (2 * kBK) == 0 && (M + 128) * K * 2 < (int64_t{1} << 31) && static_cast<int64_t>(N) * K * 2 < (int64_t{1} << 31);
+}
+
+// Split K for the large form: enough splits that its 128 x 128 tiles give one workgroup per CU
+// (each split at least two steps of kBK, an even count), as many as `ws_bytes` of fp32 partials
+// hold; 1 = no split. `steps` receives the steps per split. (Two workgroups per CU measured
+// slower: M = 1024, K = 3584, N = 512 took 28.0 against 18.7 us, the partials' HBM traffic
+// outweighing the extra parallelism.)
+int split_count(int64_t M, int32_t N, int32_t K, int64_t ws_bytes, int* steps) {
+  const int nk = K / kBK;
+  *steps = nk;
+  const int64_t tiles = (M + 127) / 128 * ((N + 127) / 128);
+  if (tiles >= kSplitTarget || nk < 4) return 1;
+  int64_t want = (kSplitTarget + tiles - 1) / tiles;
+  const int64_t fit = ws_bytes / (M * N * 4);
+  if (want > fit) want = fit;
+  if (want > nk / 2) want = nk / 2;
+  if (want <= 1) return 1;
+  const int per = static_cast<int>(((nk + want - 1) / want + 1) / 2 * 2);  // even steps per split
+  *steps = per;
+  return (nk + per - 1) / per;
+}
+
+// 128 x 256 tiles when there are at least two per CU, else 128 x 128 (split over K when even
+// those leave CUs idle); the general form for the rest.
 template <bool LN, typename PT, typename BT, typename OT>
-hipError_t launch_linear(const LinearParams& p, hipStream_t s) {
-  const bool big = p.K % (2 * kBK) == 0 && (p.M + 128) * p.K * 2 < (int64_t{1} << 31) &&
-                   static_cast<int64_t>(p.N) * p.K * 2 < (int64_t{1} << 31);
-  if (big) {
-    if ((p.M + 127) / 128 * ((p.N + 255) / 256) >= 2 * 256) return launch_big<256, 2, LN, PT, BT, OT>(p, s);
-    return launch_big<128, 2, LN, PT, BT, OT>(p, s);
+hipError_t launch_linear(const LinearParams& p, int64_t ws_bytes, hipStream_t s) {
+  if (big_form(p.M, p.N, p.K)) {
+    if ((p.M + 127) / 128 * ((p.N + 255) / 256) >= 2 * 256) return launch_big<256, 2, LN, PT, BT, OT>(p, 1, s);
+    LinearParams q = p;
+    int steps = 0;
+    const int splits = p.part ? split_count(p.M, p.N, p.K, ws_bytes, &steps) : 1;
+    q.split_steps = steps;
+    return launch_big<128, 2, LN, PT, BT, OT>(q, splits, s);
   }
   return launch_tile<64, 4, 2, LN, PT, BT, OT>(p, s);
 }
 
 template <bool LN, typename PT, typename BT>
-hipError_t launch_out(int32_t odt, const LinearParams& p, hipStream_t s) {
-  return odt == CTI_EBAG_F32 ? launch_linear<LN, PT, BT, float>(p, s) : launch_linear<LN, PT, BT, bf16_t>(p, s);
+hipError_t launch_out(int32_t odt, const LinearParams& p, int64_t ws, hipStream_t s) {
+  return odt == CTI_EBAG_F32 ? launch_linear<LN, PT, BT, float>(p, ws, s) : launch_linear<LN, PT, BT, bf16_t>(p, ws, s);
 }
 
 template <bool LN, typename PT>
-hipError_t launch_bias(int32_t bdt, int32_t odt, const LinearParams& p, hipStream_t s) {
-  return bdt == CTI_EBAG_F32 ? launch_out<LN, PT, float>(odt, p, s) : launch_out<LN, PT, bf16_t>(odt, p, s);
+hipError_t launch_bias(int32_t bdt, int32_t odt, const LinearParams& p, int64_t ws, hipStream_t s) {
+  return bdt == CTI_EBAG_F32 ? launch_out<LN, PT, float>(odt, p, ws, s) : launch_out<LN, PT, bf16_t>(odt, p, ws, s);
 }
 
 }  // namespace
@@ -482,10 +555,18 @@ hipError_t launch_bias(int32_t bdt, int32_t odt, const LinearParams& p, hipStrea
 
 using namespace cti;
 
+extern "C" int64_t cti_ebag_layernorm_linear_workspace_bytes(int64_t rows, int32_t cols, int32_t out_features) {
+  if (rows < 1 || cols < 1 || out_features < 1 || !big_form(rows, out_features, cols)) return 0;
+  int steps = 0;
+  const int splits = split_count(rows, out_features, cols, INT64_MAX, &steps);
+  return splits > 1 ? static_cast<int64_t>(splits) * rows * out_features * 4 : 0;
+}
+
 extern "C" int cti_ebag_layernorm_linear(const void* x, int64_t rows, int32_t cols, const float* mean,
                                          const float* rstd, const void* gamma, const void* beta, int32_t param_dtype,
                                          const void* weight, int32_t out_features, const void* bias,
-                                         int32_t bias_dtype, void* y, int32_t y_dtype, void* stream) {
+                                         int32_t bias_dtype, void* y, int32_t y_dtype, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
   clear_error();
   if (rows < 0) return set_error(CTI_EBAG_EINVAL, "rows must be >= 0 (got %lld)", (long long)rows);
   if (cols < 1 || out_features < 1)
@@ -506,6 +587,9 @@ extern "C" int cti_ebag_layernorm_linear(const void* x, int64_t rows, int32_t co
   const auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
   if (!a16(x) || !a16(weight) || (ln && (!a16(gamma) || !a16(beta))))
     return set_error(CTI_EBAG_EINVAL, "x, weight, gamma and beta must be 16-byte aligned");
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return set_error(CTI_EBAG_EINVAL, "workspace_bytes %lld without a workspace", (long long)workspace_bytes);
+  if (workspace && !a16(workspace)) return set_error(CTI_EBAG_EINVAL, "the workspace must be 16-byte aligned");
   if (rows > (int64_t{INT32_MAX} / 2) * 64 || (rows + 63) / 64 * ((out_features + 255) / 256) > INT32_MAX)
     return set_error(CTI_EBAG_EUNSUPPORTED, "%lld rows x %d outputs need too many tiles", (long long)rows, out_features);
   LinearParams p{};
@@ -520,12 +604,14 @@ extern "C" int cti_ebag_layernorm_linear(const void* x, int64_t rows, int32_t co
   p.M = rows;
   p.N = out_features;
   p.K = cols;
+  p.part = workspace_bytes > 0 ? static_cast<float*>(workspace) : nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   const int32_t bdt = bias ? bias_dtype : CTI_EBAG_F32;
-  if (!ln) e = launch_bias<false, float>(bdt, y_dtype, p, s);
-  else if (param_dtype == CTI_EBAG_F32) e = launch_bias<true, float>(bdt, y_dtype, p, s);
-  else e = launch_bias<true, bf16_t>(bdt, y_dtype, p, s);
+  const int64_t ws = p.part ? workspace_bytes : 0;
+  if (!ln) e = launch_bias<false, float>(bdt, y_dtype, p, ws, s);
+  else if (param_dtype == CTI_EBAG_F32) e = launch_bias<true, float>(bdt, y_dtype, p, ws, s);
+  else e = launch_bias<true, bf16_t>(bdt, y_dtype, p, ws, s);
   if (e != hipSuccess) return set_error(CTI_EBAG_EHIP, "layernorm-linear launch failed: %s", hipGetErrorString(e));
   return CTI_EBAG_OK;
 }

@@ -696,6 +696,7 @@ def layer_norm_linear(
     norm_bias: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
     out_dtype: Optional[torch.dtype] = None,
+    split_k: bool = True,
 ) -> torch.Tensor:
     """``linear(layer_norm(x))`` of the encoder in one matrix-core kernel
     (online_best/infer.py:1061-1085): ``x`` bf16 ``[rows, cols]`` (the pooled block), ``mean`` /
@@ -707,7 +708,10 @@ def layer_norm_linear(
     as it stores it, then multiplied on the matrix cores with fp32 accumulation; the normalised
     block never reaches memory. With mean, rstd, norm_weight and norm_bias all None this is the
     plain Linear. Returns ``out`` ``[rows, out_features]`` (bf16 by default, or ``out_dtype``
-    fp32), written on torch's current stream.
+    fp32), written on torch's current stream. With ``split_k`` (default) a shape whose output
+    tiles would leave CUs idle has K split over several workgroups (fp32 partials in a workspace
+    taken from torch's allocator, added in split order; a second launch), so the result can differ
+    from ``split_k=False``'s in the last bits, within fp32 accumulation.
     """
     _require_device_tensor("x", x)
     dev = x.device
@@ -748,10 +752,15 @@ def layer_norm_linear(
     if out.shape != (rows, n_out) or out.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError(f"out must be [{rows}, {n_out}] float32 / bfloat16, got {tuple(out.shape)} {out.dtype}")
     ptr = (lambda t: t.data_ptr() if t is not None else None)
+    lib = _capi.lib()
+    # K split over several workgroups when few rows would leave CUs idle: fp32 partial products
+    # in a workspace from torch's allocator (kept alive until the launches are enqueued)
+    ws_bytes = lib.cti_ebag_layernorm_linear_workspace_bytes(rows, cols, n_out) if split_k else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
     with torch.cuda.device(dev):
-        _capi.check(_capi.lib().cti_ebag_layernorm_linear(
+        _capi.check(lib.cti_ebag_layernorm_linear(
             x.data_ptr(), rows, cols, ptr(mean), ptr(rstd), ptr(norm_weight), ptr(norm_bias),
             _capi.dtype_code(norm_weight.dtype) if ln else _capi.F32, weight.data_ptr(), n_out, ptr(bias),
             _capi.dtype_code(bias.dtype) if bias is not None else _capi.F32, out.data_ptr(),
-            _capi.dtype_code(out.dtype), _capi.current_stream_handle(dev)))
+            _capi.dtype_code(out.dtype), ptr(ws), ws_bytes, _capi.current_stream_handle(dev)))
     return out

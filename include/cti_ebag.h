@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define CTI_EBAG_ABI_VERSION 4
+#define CTI_EBAG_ABI_VERSION 5
 
 /* element types of tables and outputs */
 #define CTI_EBAG_F32 0
@@ -421,12 +421,22 @@ int cti_ebag_layernorm(const void* x, void* y, int64_t rows, int64_t cols, int32
  *   weight   bf16 [out_features, cols] (nn.Linear's layout), 16-byte aligned
  *   bias     [out_features] of `bias_dtype` F32 / BF16, or NULL
  *   y        [rows, out_features] of `y_dtype` F32 / BF16, contiguous
- * The normalised block is never written to memory. Deterministic (fixed accumulation order).
+ *   workspace  device scratch of workspace_bytes (16-byte aligned), or NULL / 0: when few rows
+ *            would leave CUs idle, K is split over several workgroups per output tile, each
+ *            writing fp32 partial products here, and a second launch adds the splits in split
+ *            order, adds the bias and rounds once; as many splits are used as the workspace holds
+ *            (up to cti_ebag_layernorm_linear_workspace_bytes(...); none without a workspace)
+ * The normalised block is never written to memory. Deterministic: a given shape and workspace
+ * size always takes the same splits and accumulation order (other workspace sizes may differ in
+ * the last bits, within fp32 accumulation).
  */
 int cti_ebag_layernorm_linear(const void* x, int64_t rows, int32_t cols, const float* mean, const float* rstd,
                               const void* gamma, const void* beta, int32_t param_dtype, const void* weight,
                               int32_t out_features, const void* bias, int32_t bias_dtype, void* y,
-                              int32_t y_dtype, void* stream);
+                              int32_t y_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace cti_ebag_layernorm_linear uses at most for this shape (0: it never splits). */
+int64_t cti_ebag_layernorm_linear_workspace_bytes(int64_t rows, int32_t cols, int32_t out_features);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,8 @@ def test_header_declares_the_entry_points():
               "cti_ebag_workspace_bytes", "cti_ebag_last_error", "cti_ebag_abi_version", "cti_ebag_layernorm",
               "cti_ebag_fused_all_slots_int8", "cti_ebag_quantize_int8", "cti_ebag_fused_all_slots_typed",
               "cti_ebag_narrow_ids", "cti_ebag_stage_copy", "cti_ebag_stage_offset",
-              "cti_ebag_fused_all_slots_layernorm", "cti_ebag_order_bytes", "cti_ebag_layernorm_linear"):
+              "cti_ebag_fused_all_slots_layernorm", "cti_ebag_order_bytes", "cti_ebag_layernorm_linear",
+              "cti_ebag_layernorm_linear_workspace_bytes"):
         assert n in names
 
 
@@ -305,10 +306,10 @@ def test_layernorm_linear_rejects_bad_arguments(pkg):
 
     def call(**kw):
         a = dict(x=256, rows=4, cols=3584, mean=512, rstd=768, gamma=1024, beta=1280, pdt=c.BF16, w=1536, n=512,
-                 bias=2048, bdt=c.BF16, y=4096, ydt=c.BF16)
+                 bias=2048, bdt=c.BF16, y=4096, ydt=c.BF16, ws=None, wsb=0)
         a.update(kw)
         return f(a["x"], a["rows"], a["cols"], a["mean"], a["rstd"], a["gamma"], a["beta"], a["pdt"], a["w"], a["n"],
-                 a["bias"], a["bdt"], a["y"], a["ydt"], None)
+                 a["bias"], a["bdt"], a["y"], a["ydt"], a["ws"], a["wsb"], None)
 
     assert call(rows=-1) == c.EINVAL
     assert call(cols=0) == c.EINVAL and call(n=0) == c.EINVAL
@@ -321,8 +322,32 @@ def test_layernorm_linear_rejects_bad_arguments(pkg):
     assert call(x=264) == c.EINVAL and "aligned" in c.last_error()
     assert call(gamma=1032) == c.EINVAL
     assert call(rows=2 ** 40) == c.EUNSUPPORTED
+    assert call(wsb=1024) == c.EINVAL and "workspace" in c.last_error()  # bytes without a workspace
+    assert call(wsb=-1) == c.EINVAL
+    assert call(ws=8200, wsb=1024) == c.EINVAL and "aligned" in c.last_error()
     # nothing to do: no launch, whatever the pointers
     assert call(rows=0, x=None, w=None, y=None) == c.OK
+
+
+def test_layernorm_linear_workspace_query(pkg):
+    """Split K only for the large form (K a multiple of 128) when its 128 x 128 tiles are fewer
+    than one per CU: splits of an even number of 64-wide steps, at most half the steps."""
+    q = pkg._capi.lib().cti_ebag_layernorm_linear_workspace_bytes
+    # 32 x 4 tiles of 128 x 128 -> 2 splits of 28 steps
+    assert q(4096, 3584, 512) == 2 * 4096 * 512 * 4
+    # 8 x 4 tiles, 56 steps -> 8 wanted, 8 steps each (even) -> 7 splits
+    assert q(1024, 3584, 512) == 7 * 1024 * 512 * 4
+    # 1 x 4 tiles, 224 steps -> 64 wanted, 4 steps each -> 56 splits
+    assert q(128, 14336, 512) == 56 * 128 * 512 * 4
+    # 1 x 1 tile, 8 steps -> 256 wanted, 4 at most (two steps each)
+    assert q(64, 512, 64) == 4 * 64 * 64 * 4
+    # one tile of 128 x 128 per CU already (8192 rows): no split
+    assert q(8192, 3584, 512) == 0
+    # two or more tiles of 128 x 256 per CU: no split; K not a multiple of 128: the general form
+    assert q(32768, 3584, 512) == 0 and q(300, 136, 512) == 0
+    # too few steps to split (K = 128: two steps)
+    assert q(8, 128, 64) == 0
+    assert q(0, 3584, 512) == 0 and q(-1, 3584, 512) == 0
 
 
 def test_layernorm_statistics_only_needs_both_outputs(pkg):

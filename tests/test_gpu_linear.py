@@ -164,3 +164,29 @@ def test_rep_encoder_forward_against_the_oracle_chain(pkg, dev):
     enc.float()
     with pytest.raises(ValueError, match="fused_linear"):
         enc(batch, fused_linear=True)
+
+
+@pytest.mark.parametrize("rows,cols,n", [(129, 14336, 96), (4096, 3584, 512), (700, 1792, 512)])
+def test_split_k_against_the_unsplit_kernel(pkg, dev, rows, cols, n):
+    """K split over workgroups (fp32 partials added in split order) against one pass over K: bit
+    for bit on integer operands (every partial sum exact), within twice the fp32 accumulation
+    bound on realistic ones; the workspace the library asks for is what the wrapper uses."""
+    print(f"split-K rows={rows} cols={cols} n={n}", flush=True)
+    assert pkg._capi.lib().cti_ebag_layernorm_linear_workspace_bytes(rows, cols, n) > 0
+    rng = np.random.default_rng(rows)
+    xi = rng.integers(-1, 2, (rows, cols)).astype(np.float32)
+    wi = rng.integers(-1, 2, (n, cols)).astype(np.float32)
+    a = pkg.layer_norm_linear(_bf16(xi, dev), _bf16(wi, dev), out_dtype=torch.float32)
+    b = pkg.layer_norm_linear(_bf16(xi, dev), _bf16(wi, dev), out_dtype=torch.float32, split_k=False)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    x, gamma, beta, w, bias = _realistic(rows, cols, n, rows, dev)
+    mean, rstd = pkg.layer_norm_stats(x, 1e-5)
+    kw = dict(mean=mean, rstd=rstd, norm_weight=gamma, norm_bias=beta, out_dtype=torch.float32)
+    ys = pkg.layer_norm_linear(x, w, bias, **kw)
+    yu = pkg.layer_norm_linear(x, w, bias, split_k=False, **kw)
+    torch.cuda.synchronize()
+    _, a_op, absum = orc.layer_norm_linear_np(_np(x), _np(gamma), _np(beta), 1e-5, _np(w), _np(bias), mean=_np(mean),
+                                              rstd=_np(rstd))
+    bound = 2 * cols * 2.0 ** -23 * absum + 1e-30
+    assert np.all(np.abs(_np(ys).astype(np.float64) - _np(yu)) <= bound)
