@@ -460,16 +460,39 @@ __global__ void __launch_bounds__(8 * kWave) ln_linear_big_kernel(const LinearPa
 }
 
 // Split K: y[m, n] = (sum over splits, in split order, of the fp32 partials) + bias, one rounding.
+// Four consecutive elements per thread (16-byte loads of each split's partials; M * N is a
+// multiple of 4, so every split's block stays 16-byte aligned), the last thread taking the rest.
 template <typename BT, typename OT>
 __global__ void __launch_bounds__(256) ln_linear_reduce_kernel(const LinearParams p, int32_t splits) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= p.M * p.N) return;
-  const int n = static_cast<int>(i % p.N);
-  float v = p.part[i];
-  for (int sp = 1; sp < splits; ++sp) v += p.part[static_cast<int64_t>(sp) * p.M * p.N + i];
-  const float bn = p.bias ? Elem<BT>::load(static_cast<const char*>(p.bias) + static_cast<int64_t>(n) * Elem<BT>::kBytes)
-                          : 0.f;
-  store_y<OT>(p.y, i, v + bn);
+  const int64_t total = p.M * p.N;
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i0 >= total) return;
+  float v[4];
+  const int cnt = total - i0 < 4 ? static_cast<int>(total - i0) : 4;
+  if (total % 4 == 0) {  // then cnt == 4
+    const float4 q0 = *reinterpret_cast<const float4*>(p.part + i0);
+    v[0] = q0.x;
+    v[1] = q0.y;
+    v[2] = q0.z;
+    v[3] = q0.w;
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4 q = *reinterpret_cast<const float4*>(p.part + static_cast<int64_t>(sp) * total + i0);
+      v[0] += q.x;
+      v[1] += q.y;
+      v[2] += q.z;
+      v[3] += q.w;
+    }
+  } else {
+    for (int e = 0; e < cnt; ++e) v[e] = p.part[i0 + e];
+    for (int sp = 1; sp < splits; ++sp)
+      for (int e = 0; e < cnt; ++e) v[e] += p.part[static_cast<int64_t>(sp) * total + i0 + e];
+  }
+  for (int e = 0; e < cnt; ++e) {
+    const int n = static_cast<int>((i0 + e) % p.N);
+    const float bn = p.bias ? Elem<BT>::load(static_cast<const char*>(p.bias) + static_cast<int64_t>(n) * Elem<BT>::kBytes)
+                            : 0.f;
+    store_y<OT>(p.y, i0 + e, v[e] + bn);
+  }
 }
 
 template <int BN, int U, bool LN, typename PT, typename BT, typename OT>
@@ -482,9 +505,9 @@ hipError_t launch_big(LinearParams p, int splits, hipStream_t s) {
                      dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(splits > 1 ? splits : 1)),
                      dim3(8 * kWave), 0, s, p);
   if (splits > 1) {
-    const int64_t n = p.M * p.N;
-    hipLaunchKernelGGL((ln_linear_reduce_kernel<BT, OT>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                       s, p, splits);
+    const int64_t threads = (p.M * p.N + 3) / 4;
+    hipLaunchKernelGGL((ln_linear_reduce_kernel<BT, OT>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256),
+                       0, s, p, splits);
   }
   return hipGetLastError();
 }

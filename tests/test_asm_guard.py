@@ -18,7 +18,7 @@ SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 def test_every_hip_source_is_guarded():
     assert {"ebag_pool.hip", "ebag_layout.hip", "ebag_status.hip", "ebag_norm.hip", "ebag_quant.hip",
-            "ebag_static.hip"} <= set(SOURCES)
+            "ebag_static.hip", "ebag_linear.hip"} <= set(SOURCES)
 
 
 @pytest.mark.parametrize("src", SOURCES)

@@ -166,7 +166,7 @@ def test_rep_encoder_forward_against_the_oracle_chain(pkg, dev):
         enc(batch, fused_linear=True)
 
 
-@pytest.mark.parametrize("rows,cols,n", [(129, 14336, 96), (4096, 3584, 512), (700, 1792, 512)])
+@pytest.mark.parametrize("rows,cols,n", [(129, 14336, 96), (4096, 3584, 512), (700, 1792, 512), (129, 1792, 63)])
 def test_split_k_against_the_unsplit_kernel(pkg, dev, rows, cols, n):
     """K split over workgroups (fp32 partials added in split order) against one pass over K: bit
     for bit on integer operands (every partial sum exact), within twice the fp32 accumulation
