@@ -277,14 +277,14 @@ __device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t voff, uint32_t soff) {
 // past M or N read the last row: their products only reach accumulators that are not stored),
 // buffer loads with the step in the scalar offset, U register sets rotating, two LDS buffers, one
 // barrier per step, no branch in the loop.
-template <int BN, int U, bool LN, typename PT, typename BT, typename OT>
-__global__ void __launch_bounds__(8 * kWave) ln_linear_big_kernel(const LinearParams p) {
-  constexpr int BM = 128, THREADS = 8 * kWave;
-  constexpr int WN = BN / 4;                        // wavefront tile 64 x WN
+template <int BN, int GN, int U, bool LN, typename PT, typename BT, typename OT>
+__global__ void __launch_bounds__(2 * GN * kWave, GN == 2 ? 2 : 1) ln_linear_big_kernel(const LinearParams p) {
+  constexpr int BM = 128, THREADS = 2 * GN * kWave;  // 2 x GN wavefronts
+  constexpr int WN = BN / GN;                       // wavefront tile 64 x WN
   constexpr int MI = 4, NI = WN / 16;
-  constexpr int PA = BM * kChunks / THREADS;        // 2 x chunks per thread and step
-  constexpr int PB = BN * kChunks / THREADS;        // 4 weight chunks
-  constexpr int kRowStep = THREADS / kChunks;       // 64
+  constexpr int PA = BM * kChunks / THREADS;        // x chunks per thread and step
+  constexpr int PB = BN * kChunks / THREADS;        // weight chunks
+  constexpr int kRowStep = THREADS / kChunks;
   constexpr int PV = LN ? Elem<PT>::kBytes : 0;     // 16-byte vectors of gamma + beta per chunk
   constexpr int kStageA = BM * kLds, kStageB = BN * kLds;
   __shared__ __align__(16) uint16_t sA[2][kStageA];
@@ -300,7 +300,7 @@ __global__ void __launch_bounds__(8 * kWave) ln_linear_big_kernel(const LinearPa
   const int t = static_cast<int>(threadIdx.x);
   const int lane = t & (kWave - 1);
   const int wave = t / kWave;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / GN, wn = wave % GN;
   const int kc = t % kChunks, r0 = t / kChunks;
   const int fr = lane & 15, fk = (lane >> 4) * 8;
 
@@ -495,15 +495,15 @@ __global__ void __launch_bounds__(256) ln_linear_reduce_kernel(const LinearParam
   }
 }
 
-template <int BN, int U, bool LN, typename PT, typename BT, typename OT>
+template <int BN, int GN, int U, bool LN, typename PT, typename BT, typename OT>
 hipError_t launch_big(LinearParams p, int splits, hipStream_t s) {
   p.tiles_m = static_cast<int32_t>((p.M + 127) / 128);
   p.tiles_n = (p.N + BN - 1) / BN;
   const int64_t blocks = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
   if (splits <= 1) p.part = nullptr;
-  hipLaunchKernelGGL((ln_linear_big_kernel<BN, U, LN, PT, BT, OT>),
+  hipLaunchKernelGGL((ln_linear_big_kernel<BN, GN, U, LN, PT, BT, OT>),
                      dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(splits > 1 ? splits : 1)),
-                     dim3(8 * kWave), 0, s, p);
+                     dim3(2 * GN * kWave), 0, s, p);
   if (splits > 1) {
     const int64_t threads = (p.M * p.N + 3) / 4;
     hipLaunchKernelGGL((ln_linear_reduce_kernel<BT, OT>), dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256),
@@ -553,12 +553,12 @@ int split_count(int64_t M, int32_t N, int32_t K, int64_t ws_bytes, int* steps) {
 template <bool LN, typename PT, typename BT, typename OT>
 hipError_t launch_linear(const LinearParams& p, int64_t ws_bytes, hipStream_t s) {
   if (big_form(p.M, p.N, p.K)) {
-    if ((p.M + 127) / 128 * ((p.N + 255) / 256) >= 2 * 256) return launch_big<256, 2, LN, PT, BT, OT>(p, 1, s);
+    if ((p.M + 127) / 128 * ((p.N + 255) / 256) >= 2 * 256) return launch_big<256, 4, 2, LN, PT, BT, OT>(p, 1, s);
     LinearParams q = p;
     int steps = 0;
     const int splits = p.part ? split_count(p.M, p.N, p.K, ws_bytes, &steps) : 1;
     q.split_steps = steps;
-    return launch_big<128, 2, LN, PT, BT, OT>(q, splits, s);
+    return launch_big<128, 4, 2, LN, PT, BT, OT>(q, splits, s);
   }
   return launch_tile<64, 4, 2, LN, PT, BT, OT>(p, s);
 }
