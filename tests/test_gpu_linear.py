@@ -190,3 +190,27 @@ def test_split_k_against_the_unsplit_kernel(pkg, dev, rows, cols, n):
                                               rstd=_np(rstd))
     bound = 2 * cols * 2.0 ** -23 * absum + 1e-30
     assert np.all(np.abs(_np(ys).astype(np.float64) - _np(yu)) <= bound)
+
+
+def test_split_k_uses_as_many_splits_as_the_workspace_holds(pkg, dev):
+    """The C ABI with workspaces smaller than the queried size: fewer splits (one split's worth or
+    less: none), integer operands bit for bit against the unsplit call each time."""
+    c = pkg._capi
+    lib = c.lib()
+    rows, cols, n = 300, 3584, 512
+    full = lib.cti_ebag_layernorm_linear_workspace_bytes(rows, cols, n)
+    one = rows * n * 4  # one split's partials
+    assert full >= 4 * one
+    rng = np.random.default_rng(7)
+    x = _bf16(rng.integers(-1, 2, (rows, cols)).astype(np.float32), dev)
+    w = _bf16(rng.integers(-1, 2, (n, cols)).astype(np.float32), dev)
+    want = pkg.layer_norm_linear(x, w, out_dtype=torch.float32, split_k=False)
+    stream = c.current_stream_handle(dev)
+    for ws_bytes in (full, full // 2, 3 * one + 4096, 2 * one, one + 16, one, 16):
+        print(f"workspace {ws_bytes} bytes", flush=True)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        y = torch.full((rows, n), float("nan"), dtype=torch.float32, device=dev)
+        c.check(lib.cti_ebag_layernorm_linear(x.data_ptr(), rows, cols, None, None, None, None, c.F32, w.data_ptr(), n,
+                                              None, c.F32, y.data_ptr(), c.F32, ws.data_ptr(), ws_bytes, stream))
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), ws_bytes
