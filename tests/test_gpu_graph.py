@@ -103,3 +103,37 @@ def test_reference_layout_and_fused_layernorm_replay(pkg, dev):
             torch.cuda.synchronize()
             assert torch.equal(pooled.view(torch.int16), want_p.view(torch.int16)), rep
             assert torch.equal(normed.view(torch.int16), want_n.view(torch.int16)), rep
+
+
+@pytest.mark.parametrize("rows,cols,n", [(96, 3584, 512), (4096, 3584, 512), (300, 136, 64)])
+def test_layernorm_linear_replays(pkg, dev, rows, cols, n):
+    """Statistics pass + LayerNorm-Linear captured together: K split over workgroups (workspace from
+    the graph's pool, a GEMM and a reduction launch per call; 96 and 4096 rows), one launch
+    without a split (the general form, K not a multiple of 128). Every replay on new inputs
+    equals the eager call bit for bit."""
+    print(f"layernorm-linear replay rows={rows} cols={cols} n={n}", flush=True)
+    gen = torch.Generator().manual_seed(rows + cols)
+    xs = [(0.02 * torch.randn(rows, cols, generator=gen) + 0.01 * k).to(torch.bfloat16).to(dev) for k in range(3)]
+    gamma = (1 + 0.1 * torch.randn(cols, generator=gen)).to(torch.bfloat16).to(dev)
+    beta = (0.1 * torch.randn(cols, generator=gen)).to(torch.bfloat16).to(dev)
+    w = (torch.randn(n, cols, generator=gen) / cols ** 0.5).to(torch.bfloat16).to(dev)
+    bias = (0.1 * torch.randn(n, generator=gen)).to(torch.bfloat16).to(dev)
+    x = xs[0].clone()
+    mean = torch.empty(rows, dtype=torch.float32, device=dev)
+    rstd = torch.empty_like(mean)
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        pkg.layer_norm_stats(x, 1e-5, mean, rstd)
+        pkg.layer_norm_linear(x, w, bias, mean=mean, rstd=rstd, norm_weight=gamma, norm_bias=beta, out=out)
+
+    g = _capture(step)
+    for rep in range(2):
+        for xi in xs:
+            m, r = pkg.layer_norm_stats(xi, 1e-5)
+            want = pkg.layer_norm_linear(xi, w, bias, mean=m, rstd=r, norm_weight=gamma, norm_bias=beta).clone()
+            torch.cuda.synchronize()
+            x.copy_(xi)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int16), want.view(torch.int16)), rep
