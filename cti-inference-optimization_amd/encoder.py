@@ -105,13 +105,14 @@ class RepEncoder(nn.Module):
         """``linear(input_norm(pooled))`` (online_best/infer.py:1029-1085).
 
         By default the pooled block is normalised in place by the LayerNorm kernel and mapped by
-        ``linear`` (torch's GEMM), the fastest order measured at every timed shape: the encoder
-        shape (B = 4096, Linear 3584 -> 512), the merged 32,768-sample batch, and the reference's
-        small batches (where the library GEMM splits K over the chip). ``fused_linear=True`` takes
-        the statistics pass and the matrix-core kernel that normalises the pooled block's tiles as
-        it loads them (``layer_norm_linear``), so the normalised block never reaches memory; it
-        needs a bf16 table and a bf16 ``linear`` with LayerNorm parameters in bf16 or fp32 (the
-        reference's model after ``model.to(bfloat16)``, online_best/infer.py:2797).
+        ``linear`` (torch's GEMM), the faster order at the encoder shape (B = 4096, Linear
+        3584 -> 512) and at the merged 32,768-sample batch. ``fused_linear=True`` takes the
+        statistics pass and the matrix-core kernel that normalises the pooled block's tiles as it
+        loads them (``layer_norm_linear``, K split over the chip when the rows are few), so the
+        normalised block never reaches memory; at the reference's small warm-up batches the two
+        orders are within a few microseconds of each other. It needs a bf16 table and a bf16
+        ``linear`` with LayerNorm parameters in bf16 or fp32 (the reference's model after
+        ``model.to(bfloat16)``, online_best/infer.py:2797).
         """
         lin, norm = self.linear, self.input_norm
         if fused_linear:
