@@ -408,7 +408,8 @@ int cti_ebag_layernorm(const void* x, void* y, int64_t rows, int64_t cols, int32
                        float* mean_out, float* rstd_out, void* stream);
 
 /*
- * The input LayerNorm followed by the encoder's Linear, in one launch on the matrix cores:
+ * The input LayerNorm followed by the encoder's Linear on the matrix cores (one launch, or two
+ * when K is split over a workspace, see below):
  * replaces `norm_emb = layernorm(fused_embs)` and `rep_emb = self.linear(norm_emb)` at
  * online_best/infer.py:1061-1085 (nn.Linear(28 * D, d_model), OB:951):
  *   a[m, k] = bf16( ((x[m, k] - mean[m]) * rstd[m]) * gamma[k] + beta[k] )   (as cti_ebag_layernorm
