@@ -14,7 +14,7 @@
 // and B[8(l/16) .. +8)[l%16] and receives C[4(l/16) + r][l%16], r < 4; workgroups numbered so
 // that the tiles of one row band run on one XCD, whose L2 then serves the band to each of them):
 //   ln_linear_big_kernel  K a multiple of 128 (every encoder shape): 128 x 256 or 128 x 128 tiles
-//                         of 8 wavefronts, both operands through LDS;
+//                         of 8 wavefronts, both operands through LDS (XOR-swizzled rows);
 //   ln_linear_kernel      any K (a multiple of 8): 64 x 256 tiles of 4 wavefronts, each owning 64
 //                         columns, x through LDS and the weight's fragments straight to registers.
 // Both walk K in steps of 64 with each step's loads issued two steps ahead into rotating register
@@ -286,7 +286,10 @@ __global__ void __launch_bounds__(2 * GN * kWave, GN == 2 ? 2 : 1) ln_linear_big
   constexpr int PB = BN * kChunks / THREADS;        // weight chunks
   constexpr int kRowStep = THREADS / kChunks;
   constexpr int PV = LN ? Elem<PT>::kBytes : 0;     // 16-byte vectors of gamma + beta per chunk
-  constexpr int kStageA = BM * kLds, kStageB = BN * kLds;
+  // LDS rows of 64 elements (128 bytes), no padding: chunk c of row r sits in slot c ^ (r & 7), so
+  // the 16-byte chunk writes and the fragment reads meet no bank conflicts (2.75 M conflict cycles
+  // per launch with rows padded to 72 elements)
+  constexpr int kStageA = BM * kBK, kStageB = BN * kBK;
   __shared__ __align__(16) uint16_t sA[2][kStageA];
   __shared__ __align__(16) uint16_t sB[2][kStageB];
 
@@ -364,10 +367,10 @@ __global__ void __launch_bounds__(2 * GN * kWave, GN == 2 ? 2 : 1) ln_linear_big
     for (int q = 0; q < PA; ++q) {
       uint4 v = a[q];
       if constexpr (LN) v = normalise8(a[q], mean[q], rstd[q], g, bt);
-      *reinterpret_cast<uint4*>(&sA[buf][(r0 + q * kRowStep) * kLds + kc * 8]) = v;
+      *reinterpret_cast<uint4*>(&sA[buf][(r0 + q * kRowStep) * kBK + ((kc ^ (r0 & 7)) << 3)]) = v;
     }
 #pragma unroll
-    for (int q = 0; q < PB; ++q) *reinterpret_cast<uint4*>(&sB[buf][(r0 + q * kRowStep) * kLds + kc * 8]) = b[q];
+    for (int q = 0; q < PB; ++q) *reinterpret_cast<uint4*>(&sB[buf][(r0 + q * kRowStep) * kBK + ((kc ^ (r0 & 7)) << 3)]) = b[q];
   };
 
   f32x4 acc[MI][NI];
@@ -376,16 +379,17 @@ __global__ void __launch_bounds__(2 * GN * kWave, GN == 2 ? 2 : 1) ln_linear_big
 #pragma unroll
     for (int c = 0; c < NI; ++c) acc[a][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto multiply = [&](int buf) {
-    // every fragment of the step is read first (16 LDS reads in flight), then the products
+    // every fragment of the step is read first (16 LDS reads in flight), then the products; a
+    // fragment row's r & 7 is fr & 7 (the other terms of the row are multiples of 8)
     bf16x8 fa[2][MI], fb[2][NI];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int c = 0; c < NI; ++c)
-        fb[h][c] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn * WN + c * 16 + fr) * kLds + h * 32 + fk]);
+        fb[h][c] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn * WN + c * 16 + fr) * kBK + ((((h * 32 + fk) >> 3) ^ (fr & 7)) << 3)]);
 #pragma unroll
       for (int a = 0; a < MI; ++a)
-        fa[h][a] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm * 64 + a * 16 + fr) * kLds + h * 32 + fk]);
+        fa[h][a] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm * 64 + a * 16 + fr) * kBK + ((((h * 32 + fk) >> 3) ^ (fr & 7)) << 3)]);
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h)
